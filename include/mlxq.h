@@ -1,0 +1,174 @@
+/*
+ * mlxq.h -- C ABI of libmlxq, the MI355X (gfx950) implementation of
+ * mlx-bun's quantized-inference hot path.
+ *
+ * The TypeScript decode loop binds these symbols with bun:ffi dlopen the same
+ * way it binds libmlxc today (src/mlx/ffi.ts:26-41): plain pointers, sizes
+ * and ints, an int status per call (0 = OK), and a last-error string read on
+ * failure (the reference routes mlx-c errors through a recording handler and
+ * throws a JS Error carrying the message, src/mlx/ffi.ts:277-294, :338-348).
+ *
+ * Conventions
+ *  - Device buffers are raw device pointers (u64 in bun:ffi).  The caller
+ *    owns every buffer (mlxq_malloc / mlxq_free); array handles and their
+ *    dispose()/FinalizationRegistry lifetime stay on the TypeScript side
+ *    (src/mlx/array.ts:45-57).
+ *  - Every compute call is asynchronous on `stream` (a hipStream_t; NULL is
+ *    the library's default stream).  mlxq_synchronize is the only call that
+ *    blocks on device work (apart from the explicit host<->device copies).
+ *  - dtype codes are mlx_dtype enum values (src/mlx/ffi.ts:297-300), so the
+ *    TS layer passes MlxArray.dtype through unchanged.
+ *  - Quantized tensors use MLX's affine layout: codes packed little-endian
+ *    into uint32 (element j at bits [j*bits, (j+1)*bits)), groups of
+ *    `group_size` consecutive elements along the last axis, one T scale and
+ *    one T bias per group.
+ *  - Errors: a non-zero status leaves a message retrievable with
+ *    mlxq_last_error() (thread-local, valid until the next failing call on
+ *    the same thread).
+ */
+#ifndef MLXQ_H
+#define MLXQ_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MLXQ_ABI_VERSION 1
+
+/* dtype codes (mlx_dtype) */
+enum {
+  MLXQ_UINT32 = 3,
+  MLXQ_INT32 = 7,
+  MLXQ_FLOAT16 = 9,
+  MLXQ_FLOAT32 = 10,
+  MLXQ_BFLOAT16 = 12
+};
+
+/* status codes */
+enum {
+  MLXQ_OK = 0,
+  MLXQ_ERR_ARGUMENT = 1,    /* shape / dtype / size rejected */
+  MLXQ_ERR_UNSUPPORTED = 2, /* valid request this build does not implement */
+  MLXQ_ERR_HIP = 3,         /* HIP runtime error */
+  MLXQ_ERR_STATE = 4        /* library not initialised */
+};
+
+/* SDPA mask modes: the reference's Mask.mode (src/model/gemma4-base.ts:21-32)
+ * restricted to what the quantized path dispatches: "" (attend everything),
+ * "causal" (bottom-right aligned, createCausalMask :1595-1615).  An "array"
+ * mask with causalEquivalent=true is passed as MLXQ_MASK_CAUSAL; a sliding
+ * window mask as MLXQ_MASK_CAUSAL with window > 0. */
+enum { MLXQ_MASK_NONE = 0, MLXQ_MASK_CAUSAL = 1 };
+
+/* ---------------------------------------------------------------- runtime */
+
+/* Selects `device`, creates the default stream.  Replaces the implicit
+ * libmlxc load + default GPU stream (src/mlx/array.ts:9-10). */
+int mlxq_init(int device);
+int mlxq_abi_version(void);
+const char* mlxq_last_error(void);
+int mlxq_device_count(int* count);
+/* Name of the device code object arch this build targets ("gfx950"). */
+const char* mlxq_target_arch(void);
+
+int mlxq_malloc(void** ptr, uint64_t nbytes);
+int mlxq_free(void* ptr);
+int mlxq_memcpy_htod(void* dst, const void* src, uint64_t nbytes, void* stream);
+int mlxq_memcpy_dtoh(void* dst, const void* src, uint64_t nbytes, void* stream);
+int mlxq_memcpy_dtod(void* dst, const void* src, uint64_t nbytes, void* stream);
+/* Zero-fill by kernel (safe inside a captured HIP graph). */
+int mlxq_fill_zero(void* dst, uint64_t nbytes, void* stream);
+/* Strided 2-D copy: `rows` rows of `row_bytes`, pitches in bytes.  Used by
+ * the host cache classes for the ring reorder / trim steps. */
+int mlxq_copy_2d(void* dst, uint64_t dst_pitch, const void* src, uint64_t src_pitch,
+                 uint64_t row_bytes, uint64_t rows, void* stream);
+int mlxq_stream_create(void** stream);
+int mlxq_stream_destroy(void* stream);
+int mlxq_synchronize(void* stream);
+int mlxq_event_create(void** event);
+int mlxq_event_destroy(void* event);
+int mlxq_event_record(void* event, void* stream);
+int mlxq_event_elapsed_ms(void* start, void* stop, float* ms);
+/* HIP graph capture of the calls issued on `stream` between begin and end
+ * (the analogue of the reference's compiled decode closures,
+ * src/model/compiled-decode.ts, for launch-bound loops).  Library calls
+ * that would allocate workspace fail while capturing: run them once before
+ * capture. */
+int mlxq_graph_begin(void* stream);
+int mlxq_graph_end(void* stream, void** graph_exec);
+int mlxq_graph_launch(void* graph_exec, void* stream);
+int mlxq_graph_destroy(void* graph_exec);
+
+/* -------------------------------------------------------------- quantize */
+
+/* mx.quantize(w, group_size, bits, "affine") -- replaces mlx_quantize as
+ * bound by ops.quantize (src/mlx/ops.ts:615-641, src/mlx/ffi.ts:100).
+ * w: [rows, dim] T; packed: [rows, dim*bits/32] u32; scales/biases:
+ * [rows, dim/group_size] T.  bits in {2,4,8}, group_size in {32,64,128},
+ * T in {float16, bfloat16, float32}. */
+int mlxq_quantize(const void* w, int dtype, int64_t rows, int64_t dim, int group_size, int bits,
+                  uint32_t* packed, void* scales, void* biases, void* stream);
+
+/* Quantize `rows_per_head` new rows of each of `heads` [B*H] heads straight
+ * into a KV cache laid out [heads, capacity, .] at slot
+ * (write_pos + r) mod capacity.  One launch replaces the quantize + six
+ * slice_update calls of QuantizedKVCache.updateAndFetchQuantized
+ * (src/model/gemma4-base.ts:452-507) and of RotatingQuantizedKVCache's
+ * in-place ring write (:1026-1094). */
+int mlxq_kv_append(const void* x, int dtype, int64_t heads, int64_t rows_per_head, int64_t dim,
+                   int group_size, int bits, uint32_t* packed, void* scales, void* biases,
+                   int64_t capacity, int64_t write_pos, void* stream);
+
+/* mx.dequantize -- replaces mlx_dequantize (src/mlx/ops.ts:212-225,
+ * src/mlx/ffi.ts:163).  out: [rows, dim] T = T(scale*code + bias). */
+int mlxq_dequantize(const uint32_t* packed, const void* scales, const void* biases, int dtype,
+                    int64_t rows, int64_t dim, int group_size, int bits, void* out, void* stream);
+
+/* --------------------------------------------------------- quantized mm */
+
+/* mx.quantized_matmul -- replaces mlx_quantized_matmul as bound by
+ * ops.quantizedMatmul / quantizedMatmulQT (src/mlx/ops.ts:171-184,
+ * :760-775; src/mlx/ffi.ts:164).
+ * x: [batch, M, K] T.  transpose=1: w [w_batch, N, K*bits/32], scales/biases
+ * [w_batch, N, K/group_size] (QuantizedLinear.forward,
+ * src/model/gemma4-base.ts:120-158).  transpose=0: w [w_batch, K,
+ * N*bits/32], scales/biases [w_batch, K, N/group_size].  x batch b uses w
+ * batch b / (batch / w_batch) (MLX broadcasting of a size-1 batch axis, as
+ * quantizedSdpaUnfused's expand_dims does, :1291-1303).
+ * y: [batch, M, N] T, fp32 accumulation. */
+int mlxq_quantized_matmul(const void* x, int dtype, int64_t batch, int64_t M, int64_t K,
+                          const uint32_t* w, const void* scales, const void* biases, int64_t w_batch,
+                          int64_t N, int group_size, int bits, int transpose, void* y, void* stream);
+
+/* ------------------------------------------------------------------ sdpa */
+
+/* quantizedSdpa(q, kq, vq, scale, mask, groupSize, bits) -- replaces the
+ * dispatch of src/model/gemma4-base.ts:1560-1578 (unfused decode :1273-1340,
+ * N-tiled prefill :1356-1521, Metal flash-decoding kernel
+ * src/model/fused-decode-kernel.ts:274-312) with one entry point.
+ * q: [B, Hq, Lq, D] T; out: [B, Hq, Lq, D] T; GQA: q head h reads kv head
+ * h / (Hq/Hkv).  K/V triples are cache buffers [B, Hkv, kv_capacity, .]
+ * (the reference's fetch views read in place, no contiguous copy).
+ * Row b attends `valid` logical positions j = 0..valid-1:
+ *   valid = valid_len ? min(valid_len[b], kv_capacity) : n_kv
+ *   slot(j) = ring_offset ? (ring_offset[b] - valid + j) mod kv_capacity : j
+ * valid_len / ring_offset are device int32 [B] arrays or NULL (ring_offset
+ * is the ring write index, the rotating caches' ringIdx).  Query i is at
+ * logical position valid - Lq + i; MLXQ_MASK_CAUSAL allows j <= pos and,
+ * with window > 0, pos < j + window.
+ * Queries are scaled as the reference does (T(q * T(scale)), skipped when
+ * scale == 1); scores, softmax and both contractions accumulate in fp32. */
+int mlxq_quantized_sdpa(const void* q, int dtype, int B, int Hq, int Hkv, int Lq, int D,
+                        const uint32_t* k_packed, const void* k_scales, const void* k_biases,
+                        const uint32_t* v_packed, const void* v_scales, const void* v_biases,
+                        int64_t kv_capacity, int64_t n_kv, const int32_t* valid_len,
+                        const int32_t* ring_offset, int mask_mode, int window, float scale,
+                        int group_size, int bits, void* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MLXQ_H */

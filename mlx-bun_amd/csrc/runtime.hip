@@ -1,0 +1,256 @@
+// runtime.hip -- libmlxq runtime: init, errors, device memory, streams,
+// events and the per-device workspace.
+//
+// Mirrors the contract the reference's FFI layer relies on
+// (src/mlx/ffi.ts:3-11, :277-348): int status per call, an error message
+// recorded on the calling thread, raw handles passed as u64.
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "mlxq_internal.h"
+
+namespace mlxq {
+
+static thread_local std::string g_last_error;
+static std::mutex g_mu;
+static int g_device = -1;
+static hipStream_t g_stream = nullptr;
+static int g_cu_count = 0;
+static std::vector<Workspace> g_ws;  // indexed by device
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+
+int fail(int code, const std::string& msg) {
+  set_error(msg);
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  set_error(std::string(what) + ": " + hipGetErrorName(e) + " (" + hipGetErrorString(e) + ")");
+  return MLXQ_ERR_HIP;
+}
+
+bool initialised() { return g_device >= 0; }
+
+hipStream_t resolve_stream(void* s) { return s ? (hipStream_t)s : g_stream; }
+
+int device_cu_count() { return g_cu_count; }
+
+int workspace(size_t partial_bytes, size_t ncounters, uint32_t** counters, void** partial, hipStream_t stream) {
+  if (ncounters > kMaxCounters) return fail(MLXQ_ERR_UNSUPPORTED, "workspace: too many split-K counters");
+  const size_t cbytes = kMaxCounters * sizeof(uint32_t);
+  const size_t bytes = cbytes + partial_bytes;
+  std::lock_guard<std::mutex> lk(g_mu);
+  int dev = 0;
+  MLXQ_HIP(hipGetDevice(&dev));
+  if ((int)g_ws.size() <= dev) g_ws.resize(dev + 1);
+  Workspace& w = g_ws[dev];
+  if (w.bytes < bytes) {
+    size_t nb = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
+    nb = (nb + 4095) & ~(size_t)4095;
+    if (w.ptr) {
+      MLXQ_HIP(hipStreamSynchronize(stream));
+      MLXQ_HIP(hipFree(w.ptr));
+      w.ptr = nullptr;
+      w.bytes = 0;
+    }
+    MLXQ_HIP(hipMalloc(&w.ptr, nb));
+    MLXQ_HIP(hipMemset(w.ptr, 0, nb));
+    w.bytes = nb;
+  }
+  *counters = reinterpret_cast<uint32_t*>(w.ptr);
+  *partial = reinterpret_cast<uint8_t*>(w.ptr) + cbytes;
+  return MLXQ_OK;
+}
+
+}  // namespace mlxq
+
+using namespace mlxq;
+
+__global__ void mlxq_fill_zero_kernel(uint4* __restrict__ dst16, uint64_t n16, uint8_t* __restrict__ tail,
+                                      uint64_t ntail) {
+  uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t j = i; j < n16; j += stride) dst16[j] = make_uint4(0, 0, 0, 0);
+  if (i < ntail) tail[i] = 0;
+}
+
+extern "C" {
+
+int mlxq_init(int device) {
+  int n = 0;
+  MLXQ_HIP(hipGetDeviceCount(&n));
+  if (device < 0 || device >= n) return fail(MLXQ_ERR_ARGUMENT, "mlxq_init: device index out of range");
+  MLXQ_HIP(hipSetDevice(device));
+  hipDeviceProp_t prop;
+  MLXQ_HIP(hipGetDeviceProperties(&prop, device));
+  std::string arch = prop.gcnArchName;
+  if (arch.rfind("gfx950", 0) != 0)
+    return fail(MLXQ_ERR_UNSUPPORTED, "libmlxq is built for gfx950 only; device is " + arch);
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (!g_stream) MLXQ_HIP(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
+  g_cu_count = prop.multiProcessorCount;
+  g_device = device;
+  return MLXQ_OK;
+}
+
+int mlxq_abi_version(void) { return MLXQ_ABI_VERSION; }
+
+const char* mlxq_last_error(void) { return g_last_error.c_str(); }
+
+const char* mlxq_target_arch(void) { return "gfx950"; }
+
+int mlxq_device_count(int* count) {
+  if (!count) return fail(MLXQ_ERR_ARGUMENT, "null out-pointer");
+  MLXQ_HIP(hipGetDeviceCount(count));
+  return MLXQ_OK;
+}
+
+int mlxq_malloc(void** ptr, uint64_t nbytes) {
+  MLXQ_REQUIRE_INIT();
+  if (!ptr) return fail(MLXQ_ERR_ARGUMENT, "null out-pointer");
+  *ptr = nullptr;
+  if (nbytes == 0) nbytes = 256;  // distinct, freeable pointer for empty arrays
+  MLXQ_HIP(hipMalloc(ptr, nbytes));
+  return MLXQ_OK;
+}
+
+int mlxq_free(void* ptr) {
+  MLXQ_REQUIRE_INIT();
+  if (ptr) MLXQ_HIP(hipFree(ptr));
+  return MLXQ_OK;
+}
+
+int mlxq_memcpy_htod(void* dst, const void* src, uint64_t nbytes, void* stream) {
+  MLXQ_REQUIRE_INIT();
+  if (!nbytes) return MLXQ_OK;
+  hipStream_t s = resolve_stream(stream);
+  MLXQ_HIP(hipMemcpyAsync(dst, src, nbytes, hipMemcpyHostToDevice, s));
+  MLXQ_HIP(hipStreamSynchronize(s));  // src is pageable host memory owned by the caller
+  return MLXQ_OK;
+}
+
+int mlxq_memcpy_dtoh(void* dst, const void* src, uint64_t nbytes, void* stream) {
+  MLXQ_REQUIRE_INIT();
+  if (!nbytes) return MLXQ_OK;
+  hipStream_t s = resolve_stream(stream);
+  MLXQ_HIP(hipMemcpyAsync(dst, src, nbytes, hipMemcpyDeviceToHost, s));
+  MLXQ_HIP(hipStreamSynchronize(s));
+  return MLXQ_OK;
+}
+
+int mlxq_memcpy_dtod(void* dst, const void* src, uint64_t nbytes, void* stream) {
+  MLXQ_REQUIRE_INIT();
+  if (!nbytes) return MLXQ_OK;
+  MLXQ_HIP(hipMemcpyAsync(dst, src, nbytes, hipMemcpyDeviceToDevice, resolve_stream(stream)));
+  return MLXQ_OK;
+}
+
+int mlxq_fill_zero(void* dst, uint64_t nbytes, void* stream) {
+  MLXQ_REQUIRE_INIT();
+  if (!nbytes) return MLXQ_OK;
+  if ((uintptr_t)dst % 16) return fail(MLXQ_ERR_ARGUMENT, "mlxq_fill_zero: dst must be 16-byte aligned");
+  uint64_t n16 = nbytes / 16, ntail = nbytes % 16;
+  uint64_t blocks = (n16 + 255) / 256;
+  if (blocks < 1) blocks = 1;
+  if (blocks > 8192) blocks = 8192;
+  hipLaunchKernelGGL(mlxq_fill_zero_kernel, dim3((unsigned)blocks), dim3(256), 0, resolve_stream(stream),
+                     (uint4*)dst, n16, (uint8_t*)dst + n16 * 16, ntail);
+  MLXQ_LAUNCHED("mlxq_fill_zero_kernel");
+  return MLXQ_OK;
+}
+
+int mlxq_copy_2d(void* dst, uint64_t dst_pitch, const void* src, uint64_t src_pitch, uint64_t row_bytes,
+                 uint64_t rows, void* stream) {
+  MLXQ_REQUIRE_INIT();
+  if (!rows || !row_bytes) return MLXQ_OK;
+  if (row_bytes > dst_pitch || row_bytes > src_pitch)
+    return fail(MLXQ_ERR_ARGUMENT, "mlxq_copy_2d: row_bytes exceeds a pitch");
+  MLXQ_HIP(hipMemcpy2DAsync(dst, dst_pitch, src, src_pitch, row_bytes, rows, hipMemcpyDeviceToDevice,
+                            resolve_stream(stream)));
+  return MLXQ_OK;
+}
+
+int mlxq_stream_create(void** stream) {
+  MLXQ_REQUIRE_INIT();
+  if (!stream) return fail(MLXQ_ERR_ARGUMENT, "null out-pointer");
+  hipStream_t s;
+  MLXQ_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+  *stream = s;
+  return MLXQ_OK;
+}
+
+int mlxq_stream_destroy(void* stream) {
+  MLXQ_REQUIRE_INIT();
+  if (stream) MLXQ_HIP(hipStreamDestroy((hipStream_t)stream));
+  return MLXQ_OK;
+}
+
+int mlxq_synchronize(void* stream) {
+  MLXQ_REQUIRE_INIT();
+  MLXQ_HIP(hipStreamSynchronize(resolve_stream(stream)));
+  return MLXQ_OK;
+}
+
+int mlxq_event_create(void** event) {
+  MLXQ_REQUIRE_INIT();
+  if (!event) return fail(MLXQ_ERR_ARGUMENT, "null out-pointer");
+  hipEvent_t e;
+  MLXQ_HIP(hipEventCreate(&e));
+  *event = e;
+  return MLXQ_OK;
+}
+
+int mlxq_event_destroy(void* event) {
+  MLXQ_REQUIRE_INIT();
+  if (event) MLXQ_HIP(hipEventDestroy((hipEvent_t)event));
+  return MLXQ_OK;
+}
+
+int mlxq_event_record(void* event, void* stream) {
+  MLXQ_REQUIRE_INIT();
+  MLXQ_HIP(hipEventRecord((hipEvent_t)event, resolve_stream(stream)));
+  return MLXQ_OK;
+}
+
+int mlxq_graph_begin(void* stream) {
+  MLXQ_REQUIRE_INIT();
+  MLXQ_HIP(hipStreamBeginCapture(resolve_stream(stream), hipStreamCaptureModeRelaxed));
+  return MLXQ_OK;
+}
+
+int mlxq_graph_end(void* stream, void** graph_exec) {
+  MLXQ_REQUIRE_INIT();
+  if (!graph_exec) return fail(MLXQ_ERR_ARGUMENT, "null out-pointer");
+  hipGraph_t g = nullptr;
+  MLXQ_HIP(hipStreamEndCapture(resolve_stream(stream), &g));
+  hipGraphExec_t ge = nullptr;
+  hipError_t e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(g);
+  if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+  *graph_exec = ge;
+  return MLXQ_OK;
+}
+
+int mlxq_graph_launch(void* graph_exec, void* stream) {
+  MLXQ_REQUIRE_INIT();
+  MLXQ_HIP(hipGraphLaunch((hipGraphExec_t)graph_exec, resolve_stream(stream)));
+  return MLXQ_OK;
+}
+
+int mlxq_graph_destroy(void* graph_exec) {
+  MLXQ_REQUIRE_INIT();
+  if (graph_exec) MLXQ_HIP(hipGraphExecDestroy((hipGraphExec_t)graph_exec));
+  return MLXQ_OK;
+}
+
+int mlxq_event_elapsed_ms(void* start, void* stop, float* ms) {
+  MLXQ_REQUIRE_INIT();
+  if (!ms) return fail(MLXQ_ERR_ARGUMENT, "null out-pointer");
+  MLXQ_HIP(hipEventSynchronize((hipEvent_t)stop));
+  MLXQ_HIP(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)stop));
+  return MLXQ_OK;
+}
+
+}  // extern "C"

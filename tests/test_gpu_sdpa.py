@@ -1,0 +1,143 @@
+"""GPU: quantized SDPA against the oracle.
+
+Bar: |out - fp32 ref| <= 1e-2 + 1e-3 |ref| elementwise (fp32 accumulation
+throughout; the output itself is rounded to T).  Against the reference's
+rounding-point restatement (quantizedSdpaUnfused in T) the difference must
+stay under 0.02, the bound tests/fused-decode-kernel.test.ts:61 holds the
+reference's own fused kernel to.
+"""
+import numpy as np
+import pytest
+
+from conftest import assert_close
+
+pytestmark = pytest.mark.gpu
+
+BF16, F16, F32 = 12, 9, 10
+
+
+def rng_t(O, shape, seed, dtype, scale=1.0):
+    r = np.random.default_rng(seed)
+    return O.round_t(r.standard_normal(shape).astype(np.float32) * scale, dtype)
+
+
+def upload_triple(mlxq_dev, t, dtype):
+    from mlxq.array import DeviceArray
+    from mlxq.ops import QuantizedTensor
+
+    return QuantizedTensor(DeviceArray.fromNumpy(t[0], 3), DeviceArray.fromNumpy(t[1], dtype),
+                           DeviceArray.fromNumpy(t[2], dtype))
+
+
+def run(O, mlxq_dev, q, kq, vq, dtype, scale, gs, bits, mask=None, valid=None, ring=None):
+    from mlxq import ops
+    from mlxq.array import DeviceArray
+
+    dq = DeviceArray.fromFloat32(q, q.shape, dtype)
+    vl = DeviceArray.fromNumpy(np.asarray(valid, np.int32), 7) if valid is not None else None
+    ro = DeviceArray.fromNumpy(np.asarray(ring, np.int32), 7) if ring is not None else None
+    out = ops.quantizedSdpa(dq, upload_triple(mlxq_dev, kq, dtype), upload_triple(mlxq_dev, vq, dtype), scale,
+                            mask or ops.Mask(""), gs, bits, validLen=vl, ringOffset=ro)
+    return out.toFloat32()
+
+
+def case(O, B, Hq, Hkv, L, N, D, gs, bits, dtype, seed):
+    q = rng_t(O, (B, Hq, L, D), seed, dtype)
+    kq = O.quantize(rng_t(O, (B, Hkv, N, D), seed + 1, dtype), gs, bits, dtype)
+    vq = O.quantize(rng_t(O, (B, Hkv, N, D), seed + 2, dtype), gs, bits, dtype)
+    return q, kq, vq
+
+
+def check(O, got, q, kq, vq, dtype, scale, gs, bits, tag, **geo):
+    ref = O.sdpa(q, kq, vq, scale=scale, gs=gs, bits=bits, dtype=dtype, **geo)
+    assert_close(got, ref, what=tag)
+    if dtype != F32:
+        un = O.sdpa_unfused_t(q, kq, vq, scale=scale, gs=gs, bits=bits, dtype=dtype, **geo)
+        assert np.abs(got - un).max() < 0.02, tag
+
+
+def test_decode_8bit_fp16_1k(O, mlxq_dev):
+    """B=1, Hq=16, Hkv=4, D=128, N=1024, fp16, 8-bit group 64, scale 1/sqrt(128)."""
+    q, kq, vq = case(O, 1, 16, 4, 1, 1024, 128, 64, 8, F16, 0)
+    s = 1 / np.sqrt(128)
+    check(O, run(O, mlxq_dev, q, kq, vq, F16, s, 64, 8), q, kq, vq, F16, s, 64, 8, "c1")
+
+
+def test_decode_4bit_bf16_32k(O, mlxq_dev):
+    """B=1, Hq=32, Hkv=8, D=128, N=32768, bf16, 4-bit group 64."""
+    q, kq, vq = case(O, 1, 32, 8, 1, 32768, 128, 64, 4, BF16, 1)
+    s = 1 / np.sqrt(128)
+    check(O, run(O, mlxq_dev, q, kq, vq, BF16, s, 64, 4), q, kq, vq, BF16, s, 64, 4, "c2")
+
+
+def test_decode_batched_ring_window(O, mlxq_dev):
+    """B=32, Hq=16, Hkv=8, D=256, window 4096, per-row lengths in [512, 32768]
+    (attended: min(len, 4096)) and ring write offsets in [0, 4096)."""
+    r = np.random.default_rng(3)
+    B, W = 32, 4096
+    lens = r.integers(512, 32769, B).astype(np.int32)
+    lens[:3] = [512, 4095, 4096]
+    ring = r.integers(0, W, B).astype(np.int32)
+    q, kq, vq = case(O, B, 16, 8, 1, W, 256, 64, 4, BF16, 4)
+    got = run(O, mlxq_dev, q, kq, vq, BF16, 1.0, 64, 4, valid=lens, ring=ring)
+    check(O, got, q, kq, vq, BF16, 1.0, 64, 4, "c3", valid_len=lens, ring_off=ring)
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,N,D,gs,bits,dtype", [
+    (1, 4, 2, 333, 256, 64, 4, BF16),     # fused-decode-kernel.test.ts site shapes, N=333
+    (1, 4, 2, 333, 256, 64, 8, BF16),
+    (2, 8, 8, 77, 128, 32, 4, BF16),      # no GQA, group 32, short
+    (1, 16, 2, 1000, 128, 128, 8, F16),   # nRep 8, group 128
+    (3, 6, 3, 129, 128, 64, 4, F16),      # nRep 2, odd sizes
+    (1, 4, 1, 4100, 64, 32, 8, BF16),     # D=64
+    (1, 2, 2, 1, 128, 64, 4, BF16),       # one key
+    (1, 8, 2, 65537, 128, 64, 4, BF16),   # many chunks, ragged tail
+])
+def test_decode_shapes(O, mlxq_dev, B, Hq, Hkv, N, D, gs, bits, dtype):
+    q, kq, vq = case(O, B, Hq, Hkv, 1, N, D, gs, bits, dtype, N)
+    check(O, run(O, mlxq_dev, q, kq, vq, dtype, 0.125, gs, bits), q, kq, vq, dtype, 0.125, gs, bits, "shape")
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,N,D,gs,bits,dtype", [
+    (1, 16, 1, 333, 512, 64, 4, BF16),    # the 12B full-attention site (nRep 16, D 512)
+    (1, 4, 2, 200, 128, 64, 2, BF16),     # 2-bit
+    (1, 4, 2, 150, 128, 64, 4, F32),      # fp32 activations
+])
+def test_decode_generic_shapes(O, mlxq_dev, B, Hq, Hkv, N, D, gs, bits, dtype):
+    q, kq, vq = case(O, B, Hq, Hkv, 1, N, D, gs, bits, dtype, 9)
+    check(O, run(O, mlxq_dev, q, kq, vq, dtype, 1.0, gs, bits), q, kq, vq, dtype, 1.0, gs, bits, "generic")
+
+
+def test_decode_empty_rows_are_zero(O, mlxq_dev):
+    q, kq, vq = case(O, 3, 8, 2, 1, 64, 128, 64, 4, BF16, 5)
+    got = run(O, mlxq_dev, q, kq, vq, BF16, 1.0, 64, 4, valid=[0, 10, 0], ring=[3, 7, 0])
+    assert not got[0].any() and not got[2].any()
+    check(O, got[1:2], q[1:2], tuple(a[1:2] for a in kq), tuple(a[1:2] for a in vq), BF16, 1.0, 64, 4, "empty",
+          valid_len=np.array([10], np.int32), ring_off=np.array([7], np.int32))
+
+
+@pytest.mark.parametrize("L,N,window", [(16, 300, 0), (7, 50, 13), (64, 1217, 0), (33, 700, 100)])
+def test_prefill_causal(O, mlxq_dev, L, N, window):
+    from mlxq import ops
+
+    q, kq, vq = case(O, 1, 8, 2, L, N, 128, 64, 4, BF16, 11)
+    mask = ops.createCausalMask(L, N - L, window or None)
+    got = run(O, mlxq_dev, q, kq, vq, BF16, 0.125, 64, 4, mask=mask)
+    check(O, got, q, kq, vq, BF16, 0.125, 64, 4, "prefill", causal=True, window=window)
+
+
+def test_reference_lcg_case_tiled_bound(O, mlxq_dev):
+    """tests/fused-sdpa.test.ts 'multi-tile kv4': our prefill vs the reference's
+    tiled restatement within its 2/128 bound."""
+    from mlxq import ops
+
+    KV, nRep, L, N, D, gs, bits = 2, 4, 96, 1217, 64, 64, 4
+    H = KV * nRep
+    bf = O.BF16
+    q = O.round_t(O.lcg_floats(H * L * D, 17).reshape(1, H, L, D), bf)
+    k = O.round_t(O.lcg_floats(KV * N * D, 18).reshape(1, KV, N, D), bf)
+    v = O.round_t(O.lcg_floats(KV * N * D, 19).reshape(1, KV, N, D), bf)
+    kq, vq = O.quantize(k, gs, bits, bf), O.quantize(v, gs, bits, bf)
+    got = run(O, mlxq_dev, q, kq, vq, bf, 0.125, gs, bits, mask=ops.Mask("causal"))
+    tiled = O.sdpa_tiled_t(q, kq, vq, scale=0.125, gs=gs, bits=bits, dtype=bf, causal=True)
+    assert np.abs(got - tiled).max() <= 2 / 128

@@ -1,0 +1,235 @@
+"""Pins for the oracle's quantized matmul and attention (CPU).
+
+MLX's qmm/SDPA outputs for this path have no golden in the reference
+(goldens/fused-sdpa.bin is not shipped), so these functions are pinned by
+what the mathematics fixes, each check chosen so that a plausible mistake
+(wrong group index, transposed operand, dropped bias term, wrong GQA head
+map, off-by-one mask, ring offset sign) fails it:
+  - agreement with an independent float64 numpy evaluation on dequantized
+    operands (BLAS matmul / numpy softmax),
+  - closed forms: one key -> V row, identical keys -> mean of V, linearity,
+  - invariants the reference's own tests assert: tiled vs unfused <= 2/128
+    (tests/fused-sdpa.test.ts:98-114), fused decode vs unfused < 0.02
+    (tests/fused-decode-kernel.test.ts:30-67), array causal mask == causal.
+"""
+import numpy as np
+import pytest
+
+
+def rng_t(O, shape, seed, dtype, scale=1.0):
+    r = np.random.default_rng(seed)
+    return O.round_t(r.standard_normal(shape).astype(np.float32) * scale, dtype)
+
+
+def deq64(O, packed, scales, biases, gs, bits, dtype):
+    """float64 s*c + b from the quantized triple (independent of the oracle's
+    own dequantize path: unpack + numpy broadcasting)."""
+    c = O.unpack_codes(packed, bits).astype(np.float64)
+    s = O.from_t(scales, dtype).astype(np.float64).repeat(gs, axis=-1)
+    b = O.from_t(biases, dtype).astype(np.float64).repeat(gs, axis=-1)
+    return s * c + b
+
+
+@pytest.mark.parametrize("dtype", [12, 9, 10])
+@pytest.mark.parametrize("bits,gs", [(4, 64), (8, 64), (4, 32), (8, 128), (2, 64)])
+def test_quantize_roundtrip_error_bound(O, dtype, bits, gs):
+    w = rng_t(O, (37, 256), 1, dtype)
+    p, s, b = O.quantize(w, gs, bits, dtype)
+    d = deq64(O, p, s, b, gs, bits, dtype)
+    sv = np.abs(O.from_t(s, dtype)).astype(np.float64).repeat(gs, axis=-1)
+    eps = 2.0 ** -8 if dtype != 9 else 2.0 ** -11  # unit roundoff of T
+    if dtype == 10:
+        eps = 0.0
+    codes = O.unpack_codes(p, bits)
+    bound = 0.5 * sv + (codes * sv + np.abs(O.from_t(b, dtype)).repeat(gs, -1)) * eps + 1e-7
+    inner = (codes > 0) & (codes < (1 << bits) - 1)
+    assert np.all(np.abs(d - w)[inner] <= bound[inner])
+    # clamped codes sit at the end of the range the element lies beyond
+    # (the zero-point adjustment can shrink the step, pushing the far edge out)
+    sgn = np.sign(O.from_t(s, dtype)).repeat(gs, axis=-1)
+    top = codes == (1 << bits) - 1
+    assert np.all(((w - d) * sgn)[top] >= -bound[top])
+    assert np.all(((d - w) * sgn)[codes == 0] >= -bound[codes == 0])
+    # the group edge with the larger magnitude is represented exactly (before T rounding)
+    g = w.reshape(-1, gs)
+    edge = np.where(np.abs(g.min(1)) > np.abs(g.max(1)), g.min(1), g.max(1))
+    dg = d.reshape(-1, gs)
+    idx = np.argmax(g == edge[:, None], axis=1)
+    assert np.all(np.abs(dg[np.arange(len(idx)), idx] - edge) <= np.abs(edge) * 2 * eps + 1e-6)
+
+
+def test_dequantize_matches_closed_form(O):
+    for dtype in (12, 9):
+        w = rng_t(O, (8, 128), 2, dtype)
+        p, s, b = O.quantize(w, 64, 4, dtype)
+        np.testing.assert_array_equal(O.dequantize(p, s, b, 64, 4, dtype),
+                                      O.round_t(deq64(O, p, s, b, 64, 4, dtype), dtype))
+
+
+@pytest.mark.parametrize("transpose", [True, False])
+def test_qmm_vs_numpy_blas(O, transpose):
+    dtype, gs, bits = 12, 64, 4
+    M, K, N = 5, 256, 192
+    x = rng_t(O, (M, K), 3, dtype)
+    w = rng_t(O, (N, K) if transpose else (K, N), 4, dtype, 0.02)
+    p, s, b = O.quantize(w, gs, bits, dtype)
+    y = O.qmm(x, p, s, b, gs, bits, dtype, transpose=transpose)
+    wd = deq64(O, p, s, b, gs, bits, dtype)
+    ref = x.astype(np.float64) @ (wd.T if transpose else wd)
+    np.testing.assert_allclose(y, ref, rtol=1e-12, atol=1e-12)
+
+
+def test_qmm_batch_broadcast_and_linearity(O):
+    dtype, gs, bits = 12, 64, 8
+    x = rng_t(O, (6, 3, 128), 5, dtype)  # batch 6 over w_batch 2 (rep 3)
+    w = rng_t(O, (2, 40, 128), 6, dtype)
+    p, s, b = O.quantize(w, gs, bits, dtype)
+    y = O.qmm(x, p, s, b, gs, bits, dtype)
+    for bi in range(6):
+        yb = O.qmm(x[bi], p[bi // 3], s[bi // 3], b[bi // 3], gs, bits, dtype)
+        np.testing.assert_allclose(y[bi], yb, rtol=0, atol=0)
+    y2 = O.qmm(2 * x, p, s, b, gs, bits, dtype)
+    np.testing.assert_allclose(y2, 2 * y, rtol=1e-12, atol=1e-12)
+
+
+def numpy_sdpa(O, q, kq, vq, scale, gs, bits, dtype, causal=False, window=0, n_kv=None):
+    """Independent float64 attention over dequantized caches (GQA by head
+    repetition), bottom-right causal / window masks built with numpy."""
+    B, Hq, L, D = q.shape
+    K = deq64(O, *kq, gs, bits, dtype)
+    V = deq64(O, *vq, gs, bits, dtype)
+    if n_kv is not None:
+        K, V = K[:, :, :n_kv], V[:, :, :n_kv]
+    rep = Hq // K.shape[1]
+    K, V = np.repeat(K, rep, axis=1), np.repeat(V, rep, axis=1)
+    qs = q.astype(np.float64) if scale == 1.0 else O.round_t(q * O.round_t(np.float32(scale), dtype), dtype)
+    S = np.einsum("bhld,bhnd->bhln", qs.astype(np.float64), K)
+    N = K.shape[2]
+    pos = np.arange(N - L, N)[:, None]
+    j = np.arange(N)[None, :]
+    allow = np.ones((L, N), bool)
+    if causal:
+        allow &= j <= pos
+    if window:
+        allow &= pos < j + window
+    S = np.where(allow, S, -np.inf)
+    S = S - S.max(-1, keepdims=True)
+    P = np.exp(S)
+    P /= P.sum(-1, keepdims=True)
+    return np.einsum("bhln,bhnd->bhld", P, V)
+
+
+def make_case(O, B, Hq, Hkv, L, N, D, gs, bits, dtype, seed):
+    q = rng_t(O, (B, Hq, L, D), seed, dtype)
+    k = rng_t(O, (B, Hkv, N, D), seed + 1, dtype)
+    v = rng_t(O, (B, Hkv, N, D), seed + 2, dtype)
+    return q, O.quantize(k, gs, bits, dtype), O.quantize(v, gs, bits, dtype)
+
+
+@pytest.mark.parametrize("case", [
+    dict(B=1, Hq=16, Hkv=4, L=1, N=300, D=128, gs=64, bits=8, dtype=9, scale=128 ** -0.5),
+    dict(B=2, Hq=8, Hkv=8, L=1, N=77, D=64, gs=32, bits=4, dtype=12, scale=1.0),
+    dict(B=1, Hq=6, Hkv=2, L=9, N=130, D=128, gs=64, bits=4, dtype=12, scale=0.125, causal=True),
+    dict(B=1, Hq=4, Hkv=2, L=7, N=50, D=64, gs=64, bits=8, dtype=12, scale=1.0, causal=True, window=13),
+])
+def test_sdpa_vs_numpy(O, case):
+    c = dict(case)
+    causal, window, scale = c.pop("causal", False), c.pop("window", 0), c.pop("scale")
+    q, kq, vq = make_case(O, c["B"], c["Hq"], c["Hkv"], c["L"], c["N"], c["D"], c["gs"], c["bits"], c["dtype"], 7)
+    got = O.sdpa(q, kq, vq, scale=scale, gs=c["gs"], bits=c["bits"], dtype=c["dtype"], causal=causal, window=window)
+    ref = numpy_sdpa(O, q, kq, vq, scale, c["gs"], c["bits"], c["dtype"], causal, window)
+    np.testing.assert_allclose(got, ref, rtol=1e-9, atol=1e-9)
+
+
+def test_sdpa_closed_forms(O):
+    dtype, gs, bits = 12, 64, 4
+    q = rng_t(O, (1, 4, 1, 128), 11, dtype)
+    k = rng_t(O, (1, 2, 1, 128), 12, dtype)
+    v = rng_t(O, (1, 2, 1, 128), 13, dtype)
+    kq, vq = O.quantize(k, gs, bits, dtype), O.quantize(v, gs, bits, dtype)
+    # one key: softmax weight 1, output = dequantized V row
+    out = O.sdpa(q, kq, vq, scale=0.3, gs=gs, bits=bits, dtype=dtype)
+    vd = deq64(O, *vq, gs, bits, dtype)
+    np.testing.assert_allclose(out[0, :2, 0], np.repeat(vd[0, :1, 0], 2, 0), rtol=1e-12)
+    np.testing.assert_allclose(out[0, 2:, 0], np.repeat(vd[0, 1:, 0], 2, 0), rtol=1e-12)
+    # identical keys: uniform weights, output = mean of V rows
+    kk = np.repeat(k, 40, axis=2)
+    vv = rng_t(O, (1, 2, 40, 128), 14, dtype)
+    kq2, vq2 = O.quantize(kk, gs, bits, dtype), O.quantize(vv, gs, bits, dtype)
+    out2 = O.sdpa(q, kq2, vq2, scale=1.0, gs=gs, bits=bits, dtype=dtype)
+    vd2 = deq64(O, *vq2, gs, bits, dtype)
+    np.testing.assert_allclose(out2[0, 0, 0], vd2[0, 0].mean(0), rtol=1e-10)
+    np.testing.assert_allclose(out2[0, 3, 0], vd2[0, 1].mean(0), rtol=1e-10)
+
+
+def test_sdpa_ring_equals_rolled_linear(O):
+    """A ring row (valid, ring write index) attends the same keys as the
+    linear layout rolled into temporal order."""
+    dtype, gs, bits = 12, 64, 4
+    B, Hq, Hkv, cap, D = 3, 4, 2, 64, 128
+    q, kq, vq = make_case(O, B, Hq, Hkv, 1, cap, D, gs, bits, dtype, 21)
+    valid = np.array([64, 17, 40], np.int32)
+    ring = np.array([5, 63, 0], np.int32)
+    got = O.sdpa(q, kq, vq, scale=1.0, gs=gs, bits=bits, dtype=dtype, valid_len=valid, ring_off=ring)
+    for b in range(B):
+        slots = [(ring[b] - valid[b] + j) % cap for j in range(valid[b])]
+        kb = tuple(a[b:b + 1, :, slots] for a in kq)
+        vb = tuple(a[b:b + 1, :, slots] for a in vq)
+        ref = numpy_sdpa(O, q[b:b + 1], kb, vb, 1.0, gs, bits, dtype)
+        np.testing.assert_allclose(got[b:b + 1], ref, rtol=1e-9, atol=1e-12)
+
+
+# ---- the reference's own invariants on the _t (rounding-point) restatements
+
+LCG_CASES = [  # tests/fused-sdpa.test.ts:66-72
+    dict(KV=2, nRep=4, L=96, N=448, D=64, group=64, bits=8),
+    dict(KV=2, nRep=4, L=96, N=1217, D=64, group=64, bits=8),
+    dict(KV=2, nRep=4, L=96, N=1217, D=64, group=64, bits=4),
+    dict(KV=4, nRep=1, L=64, N=700, D=64, group=32, bits=8),
+]
+
+
+def lcg_inputs(O, c, seed):
+    H = c["KV"] * c["nRep"]
+    bf = O.BF16
+    q = O.round_t(O.lcg_floats(H * c["L"] * c["D"], seed).reshape(1, H, c["L"], c["D"]), bf)
+    k = O.round_t(O.lcg_floats(c["KV"] * c["N"] * c["D"], seed + 1).reshape(1, c["KV"], c["N"], c["D"]), bf)
+    v = O.round_t(O.lcg_floats(c["KV"] * c["N"] * c["D"], seed + 2).reshape(1, c["KV"], c["N"], c["D"]), bf)
+    return q, O.quantize(k, c["group"], c["bits"], bf), O.quantize(v, c["group"], c["bits"], bf)
+
+
+@pytest.mark.parametrize("c", LCG_CASES)
+def test_tiled_vs_unfused_within_reference_bound(O, c):
+    q, kq, vq = lcg_inputs(O, c, 17)
+    kw = dict(scale=0.125, gs=c["group"], bits=c["bits"], dtype=O.BF16, causal=True)
+    tiled = O.sdpa_tiled_t(q, kq, vq, **kw)
+    unfused = O.sdpa_unfused_t(q, kq, vq, **kw)
+    d = np.abs(tiled - unfused).max()
+    assert d <= 2 / 128, d
+    fp = O.sdpa(q, kq, vq, **kw)
+    assert np.abs(fp - unfused).max() <= 2 / 128
+
+
+def test_causal_string_equals_array_window_none(O):
+    """Bottom-right causal == createCausalMask(N, offset, None) semantics:
+    rows past the first N-L keys see one more key each."""
+    c = LCG_CASES[1]
+    q, kq, vq = lcg_inputs(O, c, 23)
+    a = O.sdpa(q, kq, vq, scale=1.0, gs=c["group"], bits=c["bits"], dtype=O.BF16, causal=True)
+    ref = numpy_sdpa(O, q, kq, vq, 1.0, c["group"], c["bits"], O.BF16, causal=True)
+    np.testing.assert_allclose(a, ref, rtol=1e-9, atol=1e-12)
+
+
+@pytest.mark.parametrize("site", [  # tests/fused-decode-kernel.test.ts:30-67
+    (4, 2, 256, 64, 4), (4, 2, 256, 64, 8), (16, 1, 512, 64, 4)])
+def test_fp32_decode_vs_unfused_within_reference_bound(O, site):
+    H, KV, D, gs, bits = site
+    N = 333
+    bf = O.BF16
+    mk = lambda shape, seed: O.round_t(O.lcg_floats(int(np.prod(shape)), seed).reshape(shape) * 0.5, bf)
+    q, k, v = mk((1, H, 1, D), 11), mk((1, KV, N, D), 22), mk((1, KV, N, D), 33)
+    kq, vq = O.quantize(k, gs, bits, bf), O.quantize(v, gs, bits, bf)
+    fp = O.sdpa(q, kq, vq, scale=1.0, gs=gs, bits=bits, dtype=bf)
+    un = O.sdpa_unfused_t(q, kq, vq, scale=1.0, gs=gs, bits=bits, dtype=bf)
+    assert np.abs(fp - un).max() < 0.02
+    assert np.abs(un).mean() > 0.001
