@@ -9,10 +9,10 @@
 //     y += s * sum_k x_k (c_k + off)  +  (b - off * s) * sum_k x_k
 // is applied to the 16x16 accumulator once per group.  sum_k x_k comes from a
 // second MFMA against a ones operand, so no VALU work depends on M.
-// x is staged once per workgroup in LDS, already permuted into the slot
-// order of the code operands.  Work: a workgroup = 4 waves x 16 weight rows,
-// the K axis optionally split over `ks` workgroups whose fp32 partials the
-// last-arriving workgroup sums in fixed order (deterministic).
+// x operands are read from global memory (L1/L2 resident; identical
+// addresses across lanes when M is small) and permuted into the codes' slot
+// order in registers.  Work: a workgroup = 16 weight rows; its waves split K
+// and reduce in LDS (deterministic, no cross-workgroup traffic).
 //
 // Everything else (transpose = false, 2-bit, group 32, fp32 activations,
 // odd shapes) takes a straightforward VALU kernel.
@@ -20,87 +20,51 @@
 
 namespace {
 
-constexpr int QMV_WAVES = 4;
-constexpr int QMV_COLS = 16 * QMV_WAVES;  // weight rows per workgroup
-constexpr int QMV_MAXT = 16;              // 64-k tiles per wave per split
+constexpr int QMV_CT = 8;  // tiles per register chunk (double-buffered)
 
-template <typename T, int BITS, int GS, int MB>
-__global__ void __launch_bounds__(256) qmv_mfma_kernel(const uint16_t* __restrict__ x, int64_t M, int64_t K,
-                                                        const uint32_t* __restrict__ w,
-                                                        const uint16_t* __restrict__ scales,
-                                                        const uint16_t* __restrict__ biases, int64_t N,
-                                                        int64_t w_rep, int64_t k_split, uint16_t* __restrict__ y,
-                                                        float* __restrict__ partial, uint32_t* __restrict__ counters) {
-  using CO = CodeOps<T, BITS>;
-  extern __shared__ __align__(16) uint8_t smem[];
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int ks = blockIdx.y;
-  const int nks = gridDim.y;
-  const int64_t bidx = blockIdx.z;
-  const int64_t wb = bidx / w_rep;
-  x += bidx * M * K;
-  y += bidx * M * N;
-  w += wb * N * (K * BITS / 32);
-  scales += wb * N * (K / GS);
-  biases += wb * N * (K / GS);
-
-  const int64_t k_begin = (int64_t)ks * k_split;
-  const int64_t k_end = min(K, k_begin + k_split);
-  const int ntiles = (int)((k_end - k_begin) / 64);
-  const int64_t chunk = k_end - k_begin;
-  const int64_t row_stride = chunk * 2 + 16;  // bytes per staged x row (+16 breaks bank aliasing)
-
-  // ---- stage x[:, k_begin:k_end] into LDS in operand slot order -----------
-  const int64_t blocks8 = chunk / 8;
-  for (int64_t i = tid; i < M * blocks8; i += blockDim.x) {
-    const int64_t m = i / blocks8, kb = i % blocks8;
-    u32x4_t d = *reinterpret_cast<const u32x4_t*>(x + m * K + k_begin + kb * 8);
-    *reinterpret_cast<u32x4_t*>(smem + m * row_stride + kb * 16) = permute8<CO::ORDER>(d);
-  }
-  __syncthreads();
-
-  // ---- this lane's weight row and codes for every tile --------------------
-  const int ln = lane & 15;       // column (weight row) within the wave's 16
-  const int lg = lane >> 4;       // lane group: k sub-range 16*lg within a tile
-  const int64_t n0 = (int64_t)blockIdx.x * QMV_COLS + wave * 16;
-  const int64_t n = n0 + ln;
-  const int64_t nl = n < N ? n : N - 1;  // clamp loads; stores are masked
-  constexpr int WPT = BITS / 2;          // packed words per lane per tile (16 codes)
-  const int64_t wrow = K * BITS / 32;
-  uint32_t wreg[QMV_MAXT][WPT];
-  float sreg[QMV_MAXT], breg[QMV_MAXT];
+// Load one chunk of QMV_CT 64-k tiles of this lane's weight row (16 codes per
+// tile) plus their scales/biases.
+template <typename T, int BITS, int GS>
+__device__ __forceinline__ void qmv_load_chunk(const uint32_t* __restrict__ wrow_ptr, const uint16_t* __restrict__ srow,
+                                               const uint16_t* __restrict__ brow, int tile0, int tile_end, int lg,
+                                               uint32_t (&wreg)[QMV_CT][BITS / 2], float (&sreg)[QMV_CT],
+                                               float (&breg)[QMV_CT]) {
+  constexpr int WPT = BITS / 2;
 #pragma unroll
-  for (int t = 0; t < QMV_MAXT; t++) {
-    if (t < ntiles) {
-      const int64_t k = k_begin + t * 64 + lg * 16;
-      const uint32_t* src = w + nl * wrow + k * BITS / 32;
+  for (int t = 0; t < QMV_CT; t++) {
+    const int tile = tile0 + t;
+    if (tile < tile_end) {
+      const uint32_t* src = wrow_ptr + ((int64_t)tile * 64 + lg * 16) * BITS / 32;
       if constexpr (WPT == 2) {
-        uint2 v = *reinterpret_cast<const uint2*>(src);
+        const uint2 v = *reinterpret_cast<const uint2*>(src);
         wreg[t][0] = v.x;
         wreg[t][WPT - 1] = v.y;
       } else {
-        uint4 v = *reinterpret_cast<const uint4*>(src);
+        const uint4 v = *reinterpret_cast<const uint4*>(src);
         wreg[t][0] = v.x;
         wreg[t][1 % WPT] = v.y;
         wreg[t][2 % WPT] = v.z;
         wreg[t][3 % WPT] = v.w;
       }
-      const int64_t gi = nl * (K / GS) + (k_begin + t * 64) / GS;
-      sreg[t] = Conv<T>::from_bits(scales[gi]);
-      breg[t] = Conv<T>::from_bits(biases[gi]);
+      sreg[t] = Conv<T>::from_bits(srow[(int64_t)tile * 64 / GS]);
+      breg[t] = Conv<T>::from_bits(brow[(int64_t)tile * 64 / GS]);
     }
   }
+}
 
+template <typename T, int BITS, int GS, int MB>
+__device__ __forceinline__ void qmv_compute_chunk(const uint16_t* __restrict__ x, int64_t M, int64_t K, int tile0,
+                                                  int tile_end, int ln, int lg,
+                                                  const uint32_t (&wreg)[QMV_CT][BITS / 2],
+                                                  const float (&sreg)[QMV_CT], const float (&breg)[QMV_CT],
+                                                  f32x4_t (&yacc)[MB]) {
+  using CO = CodeOps<T, BITS>;
+  constexpr int WPT = BITS / 2;
   const u32x4_t ones = {Mma<T>::ONES, Mma<T>::ONES, Mma<T>::ONES, Mma<T>::ONES};
-  f32x4_t yacc[MB];
 #pragma unroll
-  for (int rb = 0; rb < MB; rb++) yacc[rb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-#pragma unroll
-  for (int t = 0; t < QMV_MAXT; t++) {
-    if (t < ntiles) {
+  for (int t = 0; t < QMV_CT; t++) {
+    const int tile = tile0 + t;
+    if (tile < tile_end) {
       u32x4_t b0, b1;
       if constexpr (BITS == 4) {
         b0 = CodeOps<T, 4>::operand(wreg[t][0]);
@@ -109,66 +73,100 @@ __global__ void __launch_bounds__(256) qmv_mfma_kernel(const uint16_t* __restric
         b0 = CodeOps<T, BITS>::operand(wreg[t][0], wreg[t][1 % WPT]);
         b1 = CodeOps<T, BITS>::operand(wreg[t][2 % WPT], wreg[t][3 % WPT]);
       }
-      const float s = sreg[t];
-      const float bb = breg[t] - CO::OFFSET * s;
+      const float sc = sreg[t];
+      const float bb = breg[t] - CO::OFFSET * sc;
+      const int64_t k = (int64_t)tile * 64 + lg * 16;
 #pragma unroll
       for (int rb = 0; rb < MB; rb++) {
         int64_t m = rb * 16 + ln;
         m = m < M ? m : M - 1;
-        const uint8_t* xr = smem + m * row_stride + (t * 8 + lg * 2) * 16;
-        const u32x4_t a0 = *reinterpret_cast<const u32x4_t*>(xr);
-        const u32x4_t a1 = *reinterpret_cast<const u32x4_t*>(xr + 16);
-        // D = x (rows) . codes (cols): x is the A operand, codes the B operand
+        const uint16_t* xr = x + m * K + k;
+        const u32x4_t a0 = permute8<CO::ORDER>(*reinterpret_cast<const u32x4_t*>(xr));
+        const u32x4_t a1 = permute8<CO::ORDER>(*reinterpret_cast<const u32x4_t*>(xr + 8));
+        // D = x (A, rows m) . codes (B, cols n); the ones operand gives sum x
         f32x4_t acc = Mma<T>::mma(a0, b0, f32x4_t{0.f, 0.f, 0.f, 0.f});
         acc = Mma<T>::mma(a1, b1, acc);
         f32x4_t xs = Mma<T>::mma(a0, ones, f32x4_t{0.f, 0.f, 0.f, 0.f});
         xs = Mma<T>::mma(a1, ones, xs);
 #pragma unroll
-        for (int i = 0; i < 4; i++) yacc[rb][i] += s * acc[i] + bb * xs[i];
+        for (int i = 0; i < 4; i++) yacc[rb][i] += sc * acc[i] + bb * xs[i];
       }
+    }
+  }
+}
+
+// One workgroup = 16 weight rows (MFMA columns); its NW waves split the K
+// axis into contiguous tile ranges and their partial sums meet in LDS.  No
+// cross-workgroup traffic.  Weight codes are double-buffered in registers
+// by chunks of QMV_CT tiles so the next chunk's loads are in flight while
+// the current one computes.
+template <typename T, int BITS, int GS, int MB, int NW>
+__global__ void __launch_bounds__(NW * 64) qmv_mfma_kernel(const uint16_t* __restrict__ x, int64_t M, int64_t K,
+                                                            const uint32_t* __restrict__ w,
+                                                            const uint16_t* __restrict__ scales,
+                                                            const uint16_t* __restrict__ biases, int64_t N,
+                                                            int64_t w_rep, uint16_t* __restrict__ y) {
+  constexpr int WPT = BITS / 2;
+  __shared__ f32x4_t red[NW][MB][64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int ln = lane & 15, lg = lane >> 4;
+  const int64_t bidx = blockIdx.y;
+  const int64_t wb = bidx / w_rep;
+  x += bidx * M * K;
+  y += bidx * M * N;
+  w += wb * N * (K * BITS / 32);
+  scales += wb * N * (K / GS);
+  biases += wb * N * (K / GS);
+
+  const int64_t n = (int64_t)blockIdx.x * 16 + ln;
+  const int64_t nl = n < N ? n : N - 1;  // clamp loads; stores are masked
+  const int tiles = (int)(K / 64);
+  const int per = (tiles + NW - 1) / NW;
+  const int t_begin = min(tiles, wave * per);
+  const int t_end = min(tiles, t_begin + per);
+  const uint32_t* wrow_ptr = w + nl * (K * BITS / 32);
+  const uint16_t* srow = scales + nl * (K / GS);
+  const uint16_t* brow = biases + nl * (K / GS);
+
+  f32x4_t yacc[MB];
+#pragma unroll
+  for (int rb = 0; rb < MB; rb++) yacc[rb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  uint32_t wa[QMV_CT][WPT], wbuf[QMV_CT][WPT];
+  float sa[QMV_CT], ba[QMV_CT], sb2[QMV_CT], bb2[QMV_CT];
+  qmv_load_chunk<T, BITS, GS>(wrow_ptr, srow, brow, t_begin, t_end, lg, wa, sa, ba);
+  for (int c0 = t_begin; c0 < t_end; c0 += 2 * QMV_CT) {
+    const int c1 = c0 + QMV_CT;
+    if (c1 < t_end) qmv_load_chunk<T, BITS, GS>(wrow_ptr, srow, brow, c1, t_end, lg, wbuf, sb2, bb2);
+    qmv_compute_chunk<T, BITS, GS, MB>(x, M, K, c0, t_end, ln, lg, wa, sa, ba, yacc);
+    if (c1 < t_end) {
+      if (c1 + QMV_CT < t_end) qmv_load_chunk<T, BITS, GS>(wrow_ptr, srow, brow, c1 + QMV_CT, t_end, lg, wa, sa, ba);
+      qmv_compute_chunk<T, BITS, GS, MB>(x, M, K, c1, t_end, ln, lg, wbuf, sb2, bb2, yacc);
     }
   }
 
-  // ---- write: D layout row = 4*lg + i, col = ln ---------------------------
-  if (nks == 1) {
-    if (n < N) {
+  // ---- reduce the NW waves' partials; D layout row = 4*lg + i, col = ln ---
 #pragma unroll
-      for (int rb = 0; rb < MB; rb++)
+  for (int rb = 0; rb < MB; rb++) red[wave][rb][lane] = yacc[rb];
+  __syncthreads();
+  if (wave == 0 && n < N) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const int64_t m = rb * 16 + lg * 4 + i;
-          if (m < M) y[m * N + n] = (uint16_t)Conv<T>::to_bits(yacc[rb][i]);
-        }
-    }
-    return;
-  }
-  float* part = partial + (bidx * nks + ks) * M * N;
-  if (n < N) {
+    for (int rb = 0; rb < MB; rb++) {
+      f32x4_t acc = red[0][rb][lane];
 #pragma unroll
-    for (int rb = 0; rb < MB; rb++)
+      for (int wv = 1; wv < NW; wv++) {
+        const f32x4_t o = red[wv][rb][lane];
+        acc[0] += o[0];
+        acc[1] += o[1];
+        acc[2] += o[2];
+        acc[3] += o[3];
+      }
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const int64_t m = rb * 16 + lg * 4 + i;
-        if (m < M) part[m * N + n] = yacc[rb][i];
+        if (m < M) y[m * N + n] = (uint16_t)Conv<T>::to_bits(acc[i]);
       }
-  }
-  __threadfence();
-  __syncthreads();
-  __shared__ uint32_t last;
-  if (tid == 0) {
-    uint32_t* ctr = counters + bidx * gridDim.x + blockIdx.x;
-    last = atomicAdd(ctr, 1u) == (uint32_t)(nks - 1);
-    if (last) *ctr = 0;  // leave the counter at zero for the next launch
-  }
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
-  const int64_t ncols = min((int64_t)QMV_COLS, N - (int64_t)blockIdx.x * QMV_COLS);
-  for (int64_t i = tid; i < M * ncols; i += blockDim.x) {
-    const int64_t m = i / ncols, c = (int64_t)blockIdx.x * QMV_COLS + i % ncols;
-    float acc = 0.f;
-    for (int k = 0; k < nks; k++) acc += partial[((bidx * nks + k) * M + m) * N + c];
-    y[m * N + c] = (uint16_t)Conv<T>::to_bits(acc);
+    }
   }
 }
 
@@ -218,53 +216,40 @@ __global__ void __launch_bounds__(256) qmm_generic_kernel(const void* __restrict
   Conv<T>::store(y, m * N + n, acc);
 }
 
-template <typename T, int BITS, int GS>
-int launch_qmv(const void* x, int64_t batch, int64_t M, int64_t K, const uint32_t* w, const void* scales,
-               const void* biases, int64_t w_rep, int64_t N, void* y, hipStream_t s) {
-  const int64_t col_groups = (N + QMV_COLS - 1) / QMV_COLS;
-  const int64_t tiles = K / 64;
-  // enough k splits for ~8 waves per CU, each split at most QMV_MAXT tiles
-  const int64_t want_wgs = (int64_t)mlxq::device_cu_count() * 2;
-  int64_t nks = (want_wgs + col_groups * batch - 1) / (col_groups * batch);
-  // staged activations stay within 64 KiB of LDS
-  int64_t max_tiles = ((65536 / M) - 16) / 128;
-  if (max_tiles > QMV_MAXT) max_tiles = QMV_MAXT;
-  if (max_tiles < 1) return mlxq::fail(MLXQ_ERR_UNSUPPORTED, "qmv: M too large to stage");
-  const int64_t min_ks = (tiles + max_tiles - 1) / max_tiles;
-  if (nks < min_ks) nks = min_ks;
-  if (nks > tiles) nks = tiles;
-  if (nks < 1) nks = 1;
-  const int64_t tiles_per = (tiles + nks - 1) / nks;
-  nks = (tiles + tiles_per - 1) / tiles_per;
-  const int64_t k_split = tiles_per * 64;
-  const int64_t rows_staged = M;
-  const size_t lds = (size_t)rows_staged * (size_t)(k_split * 2 + 16);
-  if (lds > 65536) return mlxq::fail(MLXQ_ERR_UNSUPPORTED, "qmv: staged activations exceed LDS");
-  float* partial = nullptr;
-  uint32_t* counters = nullptr;
-  if (nks > 1) {
-    void* pws = nullptr;
-    const size_t pbytes = (size_t)batch * nks * M * N * sizeof(float);
-    int rc = mlxq::workspace(pbytes, (size_t)(batch * col_groups), &counters, &pws, s);
-    if (rc) return rc;
-    partial = reinterpret_cast<float*>(pws);
-  }
-  dim3 grid((unsigned)col_groups, (unsigned)nks, (unsigned)batch);
-  const int mb = (int)((M + 15) / 16);
-#define QMV_LAUNCH(MBV)                                                                                     \
-  hipLaunchKernelGGL((qmv_mfma_kernel<T, BITS, GS, MBV>), grid, dim3(256), lds, s, (const uint16_t*)x, M, K, w, \
-                     (const uint16_t*)scales, (const uint16_t*)biases, N, w_rep, k_split, (uint16_t*)y, partial,  \
-                     counters)
-  switch (mb) {
+template <typename T, int BITS, int GS, int MB>
+int launch_qmv_mb(const void* x, int64_t batch, int64_t M, int64_t K, const uint32_t* w, const void* scales,
+                  const void* biases, int64_t w_rep, int64_t N, void* y, hipStream_t s) {
+  // waves per workgroup: enough for ~8 waves per CU over the launch, capped
+  // so the LDS reduction (NW * MB KiB) stays small
+  const int64_t groups = (N + 15) / 16 * batch;
+  const int64_t want_waves = (int64_t)mlxq::device_cu_count() * 8;
+  int nw = 1;
+  while (nw < 8 && groups * nw < want_waves && (K / 64) / (2 * nw) >= 2) nw *= 2;
+  dim3 grid((unsigned)((N + 15) / 16), (unsigned)batch);
+#define QMV_LAUNCH(NWV)                                                                                      \
+  hipLaunchKernelGGL((qmv_mfma_kernel<T, BITS, GS, MB, NWV>), grid, dim3(NWV * 64), 0, s, (const uint16_t*)x, M, K, \
+                     w, (const uint16_t*)scales, (const uint16_t*)biases, N, w_rep, (uint16_t*)y)
+  switch (nw) {
     case 1: QMV_LAUNCH(1); break;
     case 2: QMV_LAUNCH(2); break;
-    case 3: QMV_LAUNCH(3); break;
     case 4: QMV_LAUNCH(4); break;
-    default: return mlxq::fail(MLXQ_ERR_UNSUPPORTED, "qmv: M > 64");
+    default: QMV_LAUNCH(8); break;
   }
 #undef QMV_LAUNCH
   MLXQ_LAUNCHED("qmv_mfma_kernel");
   return MLXQ_OK;
+}
+
+template <typename T, int BITS, int GS>
+int launch_qmv(const void* x, int64_t batch, int64_t M, int64_t K, const uint32_t* w, const void* scales,
+               const void* biases, int64_t w_rep, int64_t N, void* y, hipStream_t s) {
+  switch ((M + 15) / 16) {
+    case 1: return launch_qmv_mb<T, BITS, GS, 1>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);
+    case 2: return launch_qmv_mb<T, BITS, GS, 2>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);
+    case 3: return launch_qmv_mb<T, BITS, GS, 3>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);
+    case 4: return launch_qmv_mb<T, BITS, GS, 4>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);
+    default: return mlxq::fail(MLXQ_ERR_UNSUPPORTED, "qmv: M > 64");
+  }
 }
 
 }  // namespace

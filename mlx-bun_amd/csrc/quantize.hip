@@ -131,7 +131,7 @@ __global__ void __launch_bounds__(256) quantize_kernel(const void* __restrict__ 
   }
 }
 
-// out = T(scale * code + bias): one thread per packed word.
+// out = T(fma(scale, code, bias)): one thread per packed word.
 template <typename T, int BITS>
 __global__ void __launch_bounds__(256) dequantize_kernel(const uint32_t* __restrict__ packed, const void* __restrict__ scales,
                                                           const void* __restrict__ biases, int64_t rows, int64_t dim,
@@ -153,7 +153,7 @@ __global__ void __launch_bounds__(256) dequantize_kernel(const uint32_t* __restr
 #pragma unroll
     for (int i = 0; i < E; i++) {
       const float c = (float)((w >> (BITS * i)) & ((1u << BITS) - 1u));
-      Conv<T>::store(o, i, s * c + b);
+      Conv<T>::store(o, i, __builtin_fmaf(s, c, b));
     }
   }
 }

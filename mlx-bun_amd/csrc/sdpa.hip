@@ -257,8 +257,11 @@ __global__ void __launch_bounds__(256) sdpa_decode_mfma_kernel(
     for (int e = 1; e < 8; e++) tmax = fmaxf(tmax, s2[e]);
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-    const float m_new = fmaxf(m_run, tmax);  // finite: every tile has >= 1 valid key
-    const float alpha = exp2f(m_run - m_new);  // m_run = -inf -> 0
+    // Lazy rescale: keep the reference max unless this tile exceeds it by
+    // more than 2^8 (p stays <= 256, fp32 and T both hold that exactly as a
+    // scale); the accumulators are only rewritten when it moves.
+    const float m_new = tmax > m_run + 8.0f ? tmax : m_run;  // first tile: m_run = -inf
+    const float alpha = exp2f(m_run - m_new);                 // 1 unless moved; -inf -> 0
     m_run = m_new;
     float p[8];
     float psum = 0.f;
@@ -408,17 +411,22 @@ __global__ void __launch_bounds__(256) sdpa_decode_mfma_kernel(
   if (single) return;
 
   // ---- last chunk to arrive merges all chunks of this (b, kv head) -------
-  __threadfence();
+  // One release RMW per workgroup publishes its partial (the barrier makes
+  // every thread's stores part of thread 0's release); only the merging
+  // workgroup pays the acquire.  No full fence: that would invalidate the L2
+  // under every other workgroup still streaming K/V.
   __syncthreads();
   if (tid == 0) {
     uint32_t* ctr = counters + (int64_t)b * Hkv + kvh;
-    const uint32_t prev = atomicAdd(ctr, 1u);
+    const uint32_t prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
     last_flag = prev == (uint32_t)(nch - 1);
-    if (last_flag) *ctr = 0;
+    if (last_flag) {
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
   __syncthreads();
   if (!last_flag) return;
-  __threadfence();
   const float* parts = part + ((int64_t)b * Hkv + kvh) * gridDim.x * pstride;
   for (int idx = tid; idx < nrep * D; idx += 256) {
     const int h = idx / D, d = idx % D;

@@ -20,7 +20,8 @@
  *   - "_t" restatements reproduce the reference's rounding points (every MLX
  *     op on a T array rounds its result to T).
  *
- * Parity pins (what checks each function) are listed in oracle/README.md.
+ * Parity pins: tests/test_oracle_golden.py (reference golden vectors) and
+ * tests/test_oracle_math.py (closed forms, invariants, independent numpy).
  */
 #include <math.h>
 #include <stdint.h>
@@ -198,9 +199,11 @@ static inline uint32_t code_at(const uint32_t* row_words, int64_t d, int bits) {
 }
 
 /*
- * mx.dequantize (src/mlx/ops.ts:212-225): w = scale * code + bias per group,
- * evaluated in fp32 (scale*code is exact in fp32 for T in {f16, bf16}) and
- * rounded once to T.  Output is the T value widened to float.
+ * mx.dequantize (src/mlx/ops.ts:212-225): w = scale * code + bias per group
+ * as one fused multiply-add in fp32, rounded once to T.  For T in {f16, bf16}
+ * scale*code is exact in fp32, so fused and unfused evaluation agree; for
+ * fp32 the fused form is what MLX's `scale * q + bias` compiles to.
+ * Output is the T value widened to float.
  */
 int oracle_dequantize(const uint32_t* packed, const void* scales, const void* biases, int dtype,
                       int64_t rows, int64_t dim, int gs, int bits, float* out) {
@@ -212,7 +215,7 @@ int oracle_dequantize(const uint32_t* packed, const void* scales, const void* bi
       float s = t_load(scales, r * groups + d / gs, dtype);
       float b = t_load(biases, r * groups + d / gs, dtype);
       float c = (float)code_at(packed + r * words, d, bits);
-      out[r * dim + d] = t_round(s * c + b, dtype);
+      out[r * dim + d] = t_round(fmaf(s, c, b), dtype);
     }
   }
   return 0;

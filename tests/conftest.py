@@ -34,16 +34,29 @@ def mlxq_dev():
     return mlxq
 
 
-def assert_close(got, ref, atol=1e-2, rtol=1e-3, what=""):
-    """|got - ref| <= atol + rtol * |ref| elementwise (the attention / matmul
-    tolerance against the fp32 reference: max-abs 1e-2, relative 1e-3)."""
+def half_ulp(ref, dtype):
+    """Half a unit in the last place of T at |ref| (the rounding of an fp32
+    result to the output dtype T)."""
+    if dtype is None or dtype == 10:
+        return np.zeros_like(np.asarray(ref, dtype=np.float64))
+    mant = 7 if dtype == 12 else 10  # stored mantissa bits of bf16 / f16
+    a = np.maximum(np.abs(np.asarray(ref, dtype=np.float64)), 2.0 ** -14)
+    return 0.5 * 2.0 ** (np.floor(np.log2(a)) - mant)
+
+
+def assert_close(got, ref, atol=1e-2, rtol=1e-3, what="", dtype=None):
+    """|got - ref| <= atol + rtol |ref| (+ half an ulp of T when the output is
+    rounded to T = `dtype`): the attention / matmul bar against the fp32
+    reference -- fp32 accumulation within max-abs 1e-2 and relative 1e-3,
+    then the one rounding every T-typed output carries."""
     got = np.asarray(got, dtype=np.float64)
     ref = np.asarray(ref, dtype=np.float64)
     assert got.shape == ref.shape, (got.shape, ref.shape)
     assert np.all(np.isfinite(got)), f"{what}: non-finite output"
     err = np.abs(got - ref)
-    bad = err > atol + rtol * np.abs(ref)
+    tol = atol + rtol * np.abs(ref) + half_ulp(ref, dtype)
+    bad = err > tol
     if bad.any():
-        i = np.unravel_index(np.argmax(err - (atol + rtol * np.abs(ref))), err.shape)
+        i = np.unravel_index(np.argmax(err - tol), err.shape)
         raise AssertionError(f"{what}: {bad.sum()} / {bad.size} elements out of tolerance; worst at {i}: "
                              f"got {got[i]} ref {ref[i]} (max abs err {err.max():.3g})")
