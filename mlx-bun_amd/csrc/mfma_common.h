@@ -22,6 +22,20 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+// (x & mask) | (y & ~mask): one v_bfi_b32 when y is not a compile-time
+// constant (see opaque()).
+__device__ __forceinline__ uint32_t bfi32(uint32_t mask, uint32_t x, uint32_t y) { return (x & mask) | (y & ~mask); }
+
+// Hide a constant from the optimiser so it lives in a register and bit
+// selects against it lower to v_bfi_b32 instead of and + or.
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
 
 template <typename T>
 struct Mma;
@@ -35,9 +49,9 @@ struct Mma<BF16> {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
                                                    c, 0, 0, 0);
   }
-  // two floats -> packed pair of T (round to nearest even)
+  // two floats -> packed pair of T (round to nearest even, v_cvt_pk_bf16_f32)
   __device__ static __forceinline__ uint32_t pack2(float lo, float hi) {
-    return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
   }
 };
 
@@ -50,8 +64,8 @@ struct Mma<F16> {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
                                                   0, 0, 0);
   }
-  __device__ static __forceinline__ uint32_t pack2(float lo, float hi) {
-    return f32_to_f16_bits(lo) | (f32_to_f16_bits(hi) << 16);
+  __device__ static __forceinline__ uint32_t pack2(float lo, float hi) {  // v_cvt_pk_f16_f32
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, f16x2_t));
   }
 };
 
@@ -83,6 +97,15 @@ struct CodeOps<T, 4> {
     r.y = ((w >> 4) & 0x000f000fu) | Mma<T>::MAGIC;
     r.z = ((w >> 8) & 0x000f000fu) | Mma<T>::MAGIC;
     r.w = ((w >> 12) & 0x000f000fu) | Mma<T>::MAGIC;
+    return r;
+  }
+  // same slots, with `magic` = opaque(Mma<T>::MAGIC): 3 shifts + 4 v_bfi_b32
+  __device__ static __forceinline__ u32x4_t operand(uint32_t w, uint32_t magic) {
+    u32x4_t r;
+    r.x = bfi32(0x000f000fu, w, magic);
+    r.y = bfi32(0x000f000fu, w >> 4, magic);
+    r.z = bfi32(0x000f000fu, w >> 8, magic);
+    r.w = bfi32(0x000f000fu, w >> 12, magic);
     return r;
   }
 };

@@ -76,11 +76,10 @@ struct F32 {
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
-// round-to-nearest-even float -> bf16 bits (NaN kept quiet)
+// round-to-nearest-even float -> bf16 bits (v_cvt_pk_bf16_f32; NaN stays a
+// quiet NaN)
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
 }
 
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {

@@ -24,6 +24,9 @@
 // Everything the MFMA decode kernel does not cover (Lq > 1, D = 512 or
 // nRep * D/gs > 16, 2-bit, fp32) runs a generic VALU kernel with the same
 // semantics.
+#include <cstdlib>
+#include <initializer_list>
+
 #include "mfma_common.h"
 
 namespace {
@@ -65,28 +68,161 @@ __device__ __forceinline__ float scaled_q(float qv, float scale_t, bool apply) {
 
 // ============================================================ MFMA decode
 
-template <typename T, int BITS, int D, int GS, int TPW>
-__global__ void __launch_bounds__(256) sdpa_decode_mfma_kernel(
+template <int G>
+__device__ __forceinline__ uint16_t group_bits(const uint32_t (&o)[(G + 1) / 2], int g) {
+  return (uint16_t)(o[g >> 1] >> (16 * (g & 1)));
+}
+
+// Raw buffer resource over `bytes` bytes from `base` (gfx9 descriptor word 3
+// = 0x00020000): loads past the end return 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint32_t buf_load32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0);
+}
+__device__ __forceinline__ u32x4_t buf_load128(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
+}
+
+// One cache row's G group scales (or biases): 2G contiguous bytes.
+template <int G>
+__device__ __forceinline__ void load_row_groups_buf(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
+                                                    uint32_t (&o)[(G + 1) / 2]) {
+  if constexpr (G == 1) {
+    o[0] = __builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, (int)soff, 0);
+  } else if constexpr (G == 2) {
+    o[0] = __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0);
+  } else if constexpr (G == 4) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, (int)soff, 0);
+    o[0] = v[0];
+    o[1] = v[1];
+  } else {
+    const u32x4_t v = buf_load128(r, voff, soff);
+    o[0] = v.x;
+    o[1] = v.y;
+    o[2] = v.z;
+    o[3] = v.w;
+  }
+}
+
+// Sum over the G adjacent lanes (G-aligned) that hold the G quant-group
+// parts of one head's score: DPP quad permutes for G <= 4 (no LDS trip),
+// every lane of the group gets the same total.
+template <int G>
+__device__ __forceinline__ float group_lane_sum(float v) {
+  if constexpr (G >= 2)
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true));  // quad_perm [1,0,3,2]
+  if constexpr (G >= 4)
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true));  // quad_perm [2,3,0,1]
+  if constexpr (G >= 8) v += __shfl_xor(v, 4);
+  return v;
+}
+
+// Key chunks of one batch row.  Chunk boundaries fall on multiples of
+// `chunk` counted from the point where the row's logical window wraps to
+// slot 0 of the ring, so every chunk occupies contiguous slots: chunk c
+// covers logical keys [j0, j0 + nk) at slots [slot0, slot0 + nk).  A row
+// attends nch chunks (at most ceil(valid / chunk) + 1).
+struct ChunkRange {
+  int64_t j0, slot0;
+  int nk, nch;
+};
+
+__device__ __forceinline__ ChunkRange chunk_range(const Geometry& geo, int b, int chunk, int c) {
+  ChunkRange r;
+  const int64_t valid = row_valid(geo, b);
+  const int64_t base = row_base_slot(geo, b, valid);
+  const int64_t jw = geo.cap - base;                  // first logical key stored at slot 0
+  const int64_t off = jw < valid ? jw % chunk : 0;    // length of a leading short chunk (0: none)
+  r.nch = valid == 0 ? 0
+                     : (off == 0 ? (int)((valid + chunk - 1) / chunk) : 1 + (int)((valid - off + chunk - 1) / chunk));
+  r.j0 = off == 0 ? (int64_t)c * chunk : (c == 0 ? 0 : off + (int64_t)(c - 1) * chunk);
+  const int64_t end = (off != 0 && c == 0) ? off : min(r.j0 + chunk, valid);
+  r.nk = (int)(end - r.j0);
+  int64_t s = base + r.j0;
+  r.slot0 = s >= geo.cap ? s - geo.cap : s;
+  return r;
+}
+
+// Cross-lane reductions over the four 16-lane rows of a wave (the lanes that
+// hold the same MFMA column): v_permlane{16,32}_swap exchange rows in VALU.
+__device__ __forceinline__ float xrow_max(float v) {
+  const uint32_t u = __float_as_uint(v);
+  auto a = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const uint32_t w = __float_as_uint(v);
+  auto b = __builtin_amdgcn_permlane16_swap(w, w, false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float xrow_sum(float v) {
+  const uint32_t u = __float_as_uint(v);
+  auto a = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const uint32_t w = __float_as_uint(v);
+  auto b = __builtin_amdgcn_permlane16_swap(w, w, false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// Code tiles each decode wave keeps in flight (registers: WIN * KW words).
+#ifndef MLXQ_DECODE_WINDOW
+#define MLXQ_DECODE_WINDOW 2
+#endif
+
+// Decode tile geometry for one (T, BITS, D, GS) instance.
+template <int BITS, int D, int GS>
+struct DecodeShape {
+  static constexpr int NW = 8;               // waves per workgroup
+  static constexpr int KW = D * BITS / 32;   // packed words per cache row
+  static constexpr int G = D / GS;
+  // tiles (32 keys) per wave: up to 128/KW, with the chunk's fp32
+  // scales/biases (16 G bytes per key) held to 32 KB of LDS
+  static constexpr int TPW_REG = 128 / KW;
+  static constexpr int TPW_LDS = 2048 / (G * NW * 32);
+  static constexpr int TPW = TPW_REG < TPW_LDS ? TPW_REG : TPW_LDS;
+  static constexpr int MAXC = NW * 32 * TPW;  // keys per workgroup
+  static constexpr int WIN = MLXQ_DECODE_WINDOW;  // tiles in flight per wave
+};
+
+// One workgroup = NW waves = one chunk of up to MAXC keys of one (batch row,
+// kv head).  Wave w owns the 32-key tiles w + NW t, t < TPW.  The chunk's
+// scales/biases are loaded first and staged in LDS as fp32 (per-key
+// constants folded in once per key, not once per MFMA column); codes stream
+// through a WIN-tile register window: tile t + WIN is requested as soon as
+// tile t is consumed, so data arrives while earlier tiles compute.
+template <typename T, int BITS, int D, int GS>
+__global__ void __launch_bounds__(512) sdpa_decode_mfma_kernel(
     const uint16_t* __restrict__ q, const uint32_t* __restrict__ kp, const uint16_t* __restrict__ ksc,
     const uint16_t* __restrict__ kbi, const uint32_t* __restrict__ vp, const uint16_t* __restrict__ vsc,
     const uint16_t* __restrict__ vbi, int Hq, int Hkv, Geometry geo, float scale, int chunk,
-    uint16_t* __restrict__ out, float* __restrict__ part, uint32_t* __restrict__ counters) {
+    uint16_t* __restrict__ out, float* __restrict__ part_o, float2* __restrict__ part_ml) {
   using CO = CodeOps<T, BITS>;
-  constexpr int G = D / GS;
-  constexpr int KW = D * BITS / 32;  // packed words per cache row
+  using SH = DecodeShape<BITS, D, GS>;
+  constexpr int NW = SH::NW, TPW = SH::TPW, MAXC = SH::MAXC, G = SH::G, KW = SH::KW, WIN = SH::WIN;
+  constexpr int NT = NW * 64;
+  constexpr int GW = (G + 1) / 2;    // dwords holding one row's G group values
   constexpr int LKW = KW / 4;        // K-side words per lane (a quarter row)
   constexpr int WPS = BITS / 4;      // K-side words per k-step
   constexpr int KSTEPS = D / 32;
   constexpr int VM = KW / 16;        // V-side word columns per lane
   constexpr int E = 32 / BITS;       // codes per word
   constexpr int DT = D / 16;         // V-side MFMA tiles
-  constexpr int MAXC = 128 * TPW;    // keys per workgroup
+  constexpr int UMAX = 16 * GS;      // nrep * D <= 16 * GS
+  constexpr int KPT = (MAXC + NT - 1) / NT;  // keys staged per thread
+  constexpr float OFF = CO::OFFSET;  // code operands carry +OFF (K and V alike)
   static_assert(VM * E == DT, "tile bookkeeping");
+  static_assert(LKW % 4 == 0, "K quarter rows are whole dwordx4 loads");
+  static_assert(NT == 512, "launch bounds");
 
-  __shared__ float sb_lds[4][G][MAXC];  // K scale, K bias, V scale, V bias
-  __shared__ float u_lds[4][16 * GS];   // per-wave unnormalised outputs [wave][h*D + d] (nrep*D <= 16*GS)
-  __shared__ float m_lds[4][16], l_lds[4][16];
-  __shared__ uint32_t last_flag;
+  // sb_lds: [0] K scale * log2e, [1] (K bias - OFF * K scale) * log2e,
+  // [2] V scale, [3] V bias -- per group, per chunk key.  After the tile
+  // loop the same LDS holds u_lds, the per-wave unnormalised outputs
+  // [wave][h*D + d].
+  constexpr int SB_FLOATS = 4 * G * MAXC, U_FLOATS = NW * UMAX;
+  __shared__ float lds_raw[SB_FLOATS > U_FLOATS ? SB_FLOATS : U_FLOATS];
+  __shared__ float m_lds[NW][16], l_lds[NW][16];
+  float(&sb_lds)[4][G][MAXC] = *reinterpret_cast<float(*)[4][G][MAXC]>(lds_raw);
+  float(&u_lds)[NW][UMAX] = *reinterpret_cast<float(*)[NW][UMAX]>(lds_raw);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int ln = lane & 15, lg = lane >> 4;
@@ -94,120 +230,133 @@ __global__ void __launch_bounds__(256) sdpa_decode_mfma_kernel(
   const int nrep = Hq / Hkv;
   const int R = nrep * G;
 
-  const int64_t valid = row_valid(geo, b);
-  const int nch = (int)((valid + chunk - 1) / chunk);
-  if (c > 0 && c >= nch) return;
+  const ChunkRange cr = chunk_range(geo, b, chunk, c);
   const int64_t out_base = ((int64_t)b * Hq + (int64_t)kvh * nrep) * D;
-  if (nch == 0) {  // nothing to attend: zeros (no counter traffic)
-    for (int i = tid; i < nrep * D; i += 256) out[out_base + i] = 0;
+  if (cr.nch == 0) {  // nothing to attend: zeros
+    if (c == 0)
+      for (int i = tid; i < nrep * D; i += NT) out[out_base + i] = 0;
     return;
   }
-  const int64_t j0 = (int64_t)c * chunk;
-  const int nk = (int)min((int64_t)chunk, valid - j0);
-  const int64_t base_slot = row_base_slot(geo, b, valid);
-  const int64_t rowbase = ((int64_t)b * Hkv + kvh) * geo.cap;
+  if (c >= cr.nch) return;
+  const int nk = cr.nk;
 
-  // ---- stage this chunk's scales/biases as float, layout [array][g][key];
-  // slots past the chunk's last key read as 0 so masked keys stay finite
-  {
-    const uint16_t* arrs[4] = {ksc, kbi, vsc, vbi};
-    constexpr int per = MAXC * G;
-    for (int idx = tid; idx < 4 * per; idx += 256) {
-      const int a = idx / per, e = idx % per, key = e / G, g = e % G;
-      float val = 0.f;
-      if (key < nk) {
-        const int64_t row = rowbase + slot_of(base_slot, j0 + key, geo.cap);
-        val = Conv<T>::from_bits(arrs[a][row * G + g]);
-      }
-      sb_lds[a][g][key] = val;
-    }
-  }
-
-  // ---- q' operand (B of the score MFMA): column ln = (g, h) ---------------
+  // ---- q' operand (B of the score MFMA) -----------------------------------
+  // column ln = h * G + g: a head's G group parts sit in adjacent lanes
   const int r_me = ln;
   const bool r_ok = r_me < R;
-  const int g_me = r_ok ? r_me / nrep : G - 1;
-  const int h_me = r_ok ? r_me % nrep : 0;
+  const int g_me = r_me % G;
+  const int h_me = r_ok ? r_me / G : 0;
   const float scale_t = Conv<T>::round(scale);
   const bool apply_scale = scale != 1.0f;
+  u32x4_t qraw[KSTEPS];
+  const uint16_t* qrow = q + out_base + (int64_t)h_me * D;
+#pragma unroll
+  for (int j = 0; j < KSTEPS; j++) qraw[j] = *reinterpret_cast<const u32x4_t*>(qrow + lg * (D / 4) + 8 * j);
+
+  // ---- loads --------------------------------------------------------------
+  // Raw buffer loads whose descriptors start at the chunk's first slot and
+  // end after its last valid key: every load is a lane constant plus a
+  // scalar offset, and keys past the chunk read 0 without touching memory
+  // (their scores are masked below; zero scales/biases keep them finite).
+  const int64_t row0 = ((int64_t)b * Hkv + kvh) * geo.cap + cr.slot0;
+  const uint32_t nk32 = (uint32_t)nk;
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kp + row0 * KW, nk32 * (uint32_t)(KW * 4));
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vp + row0 * KW, nk32 * (uint32_t)(KW * 4));
+  const __amdgpu_buffer_rsrc_t rsb[4] = {make_rsrc(ksc + row0 * G, nk32 * (uint32_t)(2 * G)),
+                                         make_rsrc(kbi + row0 * G, nk32 * (uint32_t)(2 * G)),
+                                         make_rsrc(vsc + row0 * G, nk32 * (uint32_t)(2 * G)),
+                                         make_rsrc(vbi + row0 * G, nk32 * (uint32_t)(2 * G))};
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+
+  uint32_t sbreg[KPT][4][GW];
+#pragma unroll
+  for (int i = 0; i < KPT; i++) {
+    const uint32_t voff = (uint32_t)(tid + i * NT) * (2 * G);
+#pragma unroll
+    for (int a = 0; a < 4; a++) load_row_groups_buf<G>(rsb[a], voff, 0u, sbreg[i][a]);
+  }
+  __builtin_amdgcn_sched_barrier(0);  // issue order: scales/biases, then codes
+
+  uint32_t kbuf[WIN][2][LKW];  // [window slot][16-key sub-tile][words]
+  uint32_t vbuf[WIN][8][VM];   // [window slot][key e][word column]
+  // key e of a lane: e<4 -> kt + 4lg + e, e>=4 -> kt + 16 + 4lg + (e-4)
+  auto issue = [&](int t, uint32_t (&kb)[2][LKW], uint32_t (&vb)[8][VM]) {
+    const uint32_t kt = (uint32_t)((wave_u + NW * t) * 32);
+#pragma unroll
+    for (int sub = 0; sub < 2; sub++) {
+      const uint32_t voff = (uint32_t)(ln * KW + lg * LKW) * 4u;
+      const uint32_t soff = (kt + 16u * sub) * (uint32_t)(KW * 4);
+#pragma unroll
+      for (int w4 = 0; w4 < LKW; w4 += 4) {
+        const u32x4_t v = buf_load128(rk, voff + 4u * w4, soff);
+        kb[sub][w4] = v.x;
+        kb[sub][w4 + 1] = v.y;
+        kb[sub][w4 + 2] = v.z;
+        kb[sub][w4 + 3] = v.w;
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      const uint32_t koff = (uint32_t)(e < 4 ? 4 * lg + e : 16 + 4 * lg + (e - 4));
+      const uint32_t voff = (koff * KW + ln) * 4u;
+#pragma unroll
+      for (int m = 0; m < VM; m++) vb[e][m] = buf_load32(rv, voff + 64u * m, kt * (uint32_t)(KW * 4));
+    }
+  };
+#pragma unroll
+  for (int t = 0; t < WIN && t < TPW; t++) issue(t, kbuf[t], vbuf[t]);
+  __builtin_amdgcn_sched_barrier(0);  // the window is in flight before the first wait
+
+  // ---- stage scales/biases (fp32, per-key constants folded in) ------------
+#pragma unroll
+  for (int i = 0; i < KPT; i++) {
+    const int key = tid + i * NT;
+    // (the bound check is compiled only where threads outnumber slots: a
+    // branch here would let the compiler sink the loads behind it)
+    if (MAXC % NT == 0 || key < MAXC) {
+#pragma unroll
+      for (int g = 0; g < G; g++) {
+        const float ks = Conv<T>::from_bits(group_bits<G>(sbreg[i][0], g));
+        const float kb = Conv<T>::from_bits(group_bits<G>(sbreg[i][1], g));
+        sb_lds[0][g][key] = ks * LOG2E;
+        sb_lds[1][g][key] = (kb - OFF * ks) * LOG2E;
+        sb_lds[2][g][key] = Conv<T>::from_bits(group_bits<G>(sbreg[i][2], g));
+        sb_lds[3][g][key] = Conv<T>::from_bits(group_bits<G>(sbreg[i][3], g));
+      }
+    }
+  }
   u32x4_t qop[KSTEPS];
   float qsum = 0.f;
-  {
-    const uint16_t* qrow = q + out_base + (int64_t)h_me * D;
 #pragma unroll
-    for (int j = 0; j < KSTEPS; j++) {
-      const int d0 = lg * (D / 4) + 8 * j;
-      const bool in_group = r_ok && (d0 / GS == g_me);
-      u32x4_t raw = *reinterpret_cast<const u32x4_t*>(qrow + d0);
-      uint32_t wv[4] = {raw.x, raw.y, raw.z, raw.w};
+  for (int j = 0; j < KSTEPS; j++) {
+    const int d0 = lg * (D / 4) + 8 * j;
+    const bool in_group = r_ok && (d0 / GS == g_me);
+    uint32_t wv[4] = {qraw[j].x, qraw[j].y, qraw[j].z, qraw[j].w};
 #pragma unroll
-      for (int p = 0; p < 4; p++) {
-        const float lo = scaled_q<T>(Conv<T>::from_bits(wv[p] & 0xffffu), scale_t, apply_scale);
-        const float hi = scaled_q<T>(Conv<T>::from_bits(wv[p] >> 16), scale_t, apply_scale);
-        wv[p] = in_group ? Mma<T>::pack2(lo, hi) : 0u;
-        qsum += in_group ? lo + hi : 0.f;
-      }
-      qop[j] = permute8<CO::ORDER>(u32x4_t{wv[0], wv[1], wv[2], wv[3]});
+    for (int p = 0; p < 4; p++) {
+      const float lo = scaled_q<T>(Conv<T>::from_bits(wv[p] & 0xffffu), scale_t, apply_scale);
+      const float hi = scaled_q<T>(Conv<T>::from_bits(wv[p] >> 16), scale_t, apply_scale);
+      wv[p] = in_group ? Mma<T>::pack2(lo, hi) : 0u;
+      qsum += in_group ? lo + hi : 0.f;
     }
-    qsum += __shfl_xor(qsum, 16);
-    qsum += __shfl_xor(qsum, 32);
+    qop[j] = permute8<CO::ORDER>(u32x4_t{wv[0], wv[1], wv[2], wv[3]});
   }
+  qsum = xrow_sum(qsum);
+  const uint32_t magic = opaque(Mma<T>::MAGIC);
+  const u32x4_t ones = {Mma<T>::ONES, Mma<T>::ONES, Mma<T>::ONES, Mma<T>::ONES};
   __syncthreads();  // sb_lds ready
 
-  // ---- issue every load of this wave's tiles up front ---------------------
-  // tile t of this wave covers chunk keys [(wave + 4t) * 32, +32)
-  uint32_t kreg[TPW][2][LKW];
-  uint32_t vreg[TPW][8][VM];
-#pragma unroll
-  for (int t = 0; t < TPW; t++) {
-    const int kt = (wave + 4 * t) * 32;
-    if (kt < nk) {
-#pragma unroll
-      for (int sub = 0; sub < 2; sub++) {
-        int key = kt + 16 * sub + ln;
-        key = key < nk ? key : nk - 1;
-        const uint32_t* src = kp + (rowbase + slot_of(base_slot, j0 + key, geo.cap)) * KW + lg * LKW;
-#pragma unroll
-        for (int w4 = 0; w4 < LKW; w4 += 4) {
-          if constexpr (LKW >= 4) {
-            const uint4 v = *reinterpret_cast<const uint4*>(src + w4);
-            kreg[t][sub][w4] = v.x;
-            kreg[t][sub][w4 + 1] = v.y;
-            kreg[t][sub][w4 + 2] = v.z;
-            kreg[t][sub][w4 + 3] = v.w;
-          }
-        }
-        if constexpr (LKW == 2) {
-          const uint2 v = *reinterpret_cast<const uint2*>(src);
-          kreg[t][sub][0] = v.x;
-          kreg[t][sub][1] = v.y;
-        }
-      }
-#pragma unroll
-      for (int e = 0; e < 8; e++) {
-        int key = kt + (e < 4 ? 4 * lg + e : 16 + 4 * lg + (e - 4));
-        key = key < nk ? key : nk - 1;
-        const uint32_t* src = vp + (rowbase + slot_of(base_slot, j0 + key, geo.cap)) * KW;
-#pragma unroll
-        for (int m = 0; m < VM; m++) vreg[t][e][m] = src[16 * m + ln];
-      }
-    }
-  }
-
   // ---- per-wave online softmax state --------------------------------------
-  float m_run = -INFINITY;  // per head h_me (log2 domain), replicated over g and lane groups
+  float m_run = -INFINITY;  // per head h_me (log2 domain), replicated over g and lane rows
   float l_run = 0.f;        // partial over this lane's keys
-  float sp_run = 0.f;       // sum of T(p * s_v) over this lane's k slots, row r_me
   float pb_run = 0.f;       // sum of p * b_v over this lane's keys, row r_me
   f32x4_t oacc[DT];
+  f32x4_t spacc = {0.f, 0.f, 0.f, 0.f};  // sum of the A operand per row (the +OFF correction)
 #pragma unroll
   for (int i = 0; i < DT; i++) oacc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-#pragma unroll
-  for (int t = 0; t < TPW; t++) {
-    const int kt = (wave + 4 * t) * 32;
-    if (kt >= nk) continue;  // wave-uniform
-
+  auto compute = [&](int t, const uint32_t (&kb)[2][LKW], const uint32_t (&vb)[8][VM]) {
+    const int kt = (wave_u + NW * t) * 32;
     // scores: two 16-key sub-tiles, D/32 k-steps each
     f32x4_t sacc[2];
 #pragma unroll
@@ -217,115 +366,104 @@ __global__ void __launch_bounds__(256) sdpa_decode_mfma_kernel(
       for (int j = 0; j < KSTEPS; j++) {
         u32x4_t a;
         if constexpr (BITS == 4)
-          a = CodeOps<T, 4>::operand(kreg[t][sub][j * WPS]);
+          a = CodeOps<T, 4>::operand(kb[sub][j * WPS], magic);
         else
-          a = CodeOps<T, BITS>::operand(kreg[t][sub][j * WPS], kreg[t][sub][j * WPS + WPS - 1]);
+          a = CodeOps<T, BITS>::operand(kb[sub][j * WPS], kb[sub][j * WPS + WPS - 1]);
         acc = Mma<T>::mma(a, qop[j], acc);
       }
       sacc[sub] = acc;
     }
 
-    // key e of this lane: e<4 -> kt + 4lg + e, e>=4 -> kt + 16 + 4lg + (e-4)
     float s2[8];
-    float kscale[8], kbias[8];
     {
-      const float4 s_a = *reinterpret_cast<const float4*>(&sb_lds[0][g_me][kt + 4 * lg]);
-      const float4 s_b = *reinterpret_cast<const float4*>(&sb_lds[0][g_me][kt + 16 + 4 * lg]);
-      const float4 b_a = *reinterpret_cast<const float4*>(&sb_lds[1][g_me][kt + 4 * lg]);
-      const float4 b_b = *reinterpret_cast<const float4*>(&sb_lds[1][g_me][kt + 16 + 4 * lg]);
-      kscale[0] = s_a.x; kscale[1] = s_a.y; kscale[2] = s_a.z; kscale[3] = s_a.w;
-      kscale[4] = s_b.x; kscale[5] = s_b.y; kscale[6] = s_b.z; kscale[7] = s_b.w;
-      kbias[0] = b_a.x; kbias[1] = b_a.y; kbias[2] = b_a.z; kbias[3] = b_a.w;
-      kbias[4] = b_b.x; kbias[5] = b_b.y; kbias[6] = b_b.z; kbias[7] = b_b.w;
+      const float4 ka = *reinterpret_cast<const float4*>(&sb_lds[0][g_me][kt + 4 * lg]);
+      const float4 kc = *reinterpret_cast<const float4*>(&sb_lds[0][g_me][kt + 16 + 4 * lg]);
+      const float4 ba = *reinterpret_cast<const float4*>(&sb_lds[1][g_me][kt + 4 * lg]);
+      const float4 bc = *reinterpret_cast<const float4*>(&sb_lds[1][g_me][kt + 16 + 4 * lg]);
+      const float ks[8] = {ka.x, ka.y, ka.z, ka.w, kc.x, kc.y, kc.z, kc.w};
+      const float kd[8] = {ba.x, ba.y, ba.z, ba.w, bc.x, bc.y, bc.z, bc.w};
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const float cdot = e < 4 ? sacc[0][e] : sacc[1][e - 4];
+        // this group's part of key e's score for head h_me (log2 domain),
+        // summed over the head's G adjacent group lanes
+        s2[e] = group_lane_sum<G>(__builtin_fmaf(ks[e], cdot, kd[e] * qsum));
+      }
     }
+    if (kt + 32 > nk) {  // the chunk's last, partial tile (wave-uniform)
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
-      const float cdot = e < 4 ? sacc[0][e] : sacc[1][e - 4];
-      // this quant group's part of the score of key e for head h_me
-      float part_g = kscale[e] * cdot + (kbias[e] - CO::OFFSET * kscale[e]) * qsum;
-      // sum over groups: columns (g', h_me) of this lane's 16-lane row
-      float tot = 0.f;
-#pragma unroll
-      for (int gg = 0; gg < G; gg++) tot += __shfl(part_g, (lane & 48) + gg * nrep + h_me);
-      const int key = kt + (e < 4 ? 4 * lg + e : 12 + 4 * lg + e);
-      s2[e] = key < nk ? tot * LOG2E : -INFINITY;
+      for (int e = 0; e < 8; e++) {
+        const int key = kt + (e < 4 ? 4 * lg + e : 12 + 4 * lg + e);
+        s2[e] = key < nk ? s2[e] : -INFINITY;
+      }
     }
 
     // online softmax over this tile's 32 keys
-    float tmax = s2[0];
-#pragma unroll
-    for (int e = 1; e < 8; e++) tmax = fmaxf(tmax, s2[e]);
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    float tmax = fmaxf(fmaxf(fmaxf(s2[0], s2[1]), fmaxf(s2[2], s2[3])), fmaxf(fmaxf(s2[4], s2[5]), fmaxf(s2[6], s2[7])));
+    tmax = xrow_max(tmax);
     // Lazy rescale: keep the reference max unless this tile exceeds it by
     // more than 2^8 (p stays <= 256, fp32 and T both hold that exactly as a
     // scale); the accumulators are only rewritten when it moves.
-    const float m_new = tmax > m_run + 8.0f ? tmax : m_run;  // first tile: m_run = -inf
-    const float alpha = exp2f(m_run - m_new);                 // 1 unless moved; -inf -> 0
+    const float m_old = m_run;
+    const float m_new = tmax > m_old + 8.0f ? tmax : m_old;  // first tile: m_old = -inf
+    const float alpha = __builtin_amdgcn_exp2f(m_old - m_new);  // 1 unless moved; -inf -> 0
     m_run = m_new;
     float p[8];
-    float psum = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
-      p[e] = exp2f(s2[e] - m_new);
-      psum += p[e];
-    }
-    l_run = l_run * alpha + psum;
+    for (int e = 0; e < 8; e++) p[e] = __builtin_amdgcn_exp2f(s2[e] - m_new);
+    l_run = l_run * alpha + (((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7])));
 
-    // value-side A operand: row (g_me, h_me) = p * s_v, rounded to T
-    float vscale[8], vbias[8];
+    // value-side A operand: row (h_me, g_me) = T(p * s_v); bias term in fp32
+    u32x4_t aop;
     {
-      const float4 s_a = *reinterpret_cast<const float4*>(&sb_lds[2][g_me][kt + 4 * lg]);
-      const float4 s_b = *reinterpret_cast<const float4*>(&sb_lds[2][g_me][kt + 16 + 4 * lg]);
-      const float4 b_a = *reinterpret_cast<const float4*>(&sb_lds[3][g_me][kt + 4 * lg]);
-      const float4 b_b = *reinterpret_cast<const float4*>(&sb_lds[3][g_me][kt + 16 + 4 * lg]);
-      vscale[0] = s_a.x; vscale[1] = s_a.y; vscale[2] = s_a.z; vscale[3] = s_a.w;
-      vscale[4] = s_b.x; vscale[5] = s_b.y; vscale[6] = s_b.z; vscale[7] = s_b.w;
-      vbias[0] = b_a.x; vbias[1] = b_a.y; vbias[2] = b_a.z; vbias[3] = b_a.w;
-      vbias[4] = b_b.x; vbias[5] = b_b.y; vbias[6] = b_b.z; vbias[7] = b_b.w;
+      const float4 sa = *reinterpret_cast<const float4*>(&sb_lds[2][g_me][kt + 4 * lg]);
+      const float4 sc = *reinterpret_cast<const float4*>(&sb_lds[2][g_me][kt + 16 + 4 * lg]);
+      const float4 va = *reinterpret_cast<const float4*>(&sb_lds[3][g_me][kt + 4 * lg]);
+      const float4 vc = *reinterpret_cast<const float4*>(&sb_lds[3][g_me][kt + 16 + 4 * lg]);
+      aop.x = Mma<T>::pack2(p[0] * sa.x, p[1] * sa.y);
+      aop.y = Mma<T>::pack2(p[2] * sa.z, p[3] * sa.w);
+      aop.z = Mma<T>::pack2(p[4] * sc.x, p[5] * sc.y);
+      aop.w = Mma<T>::pack2(p[6] * sc.z, p[7] * sc.w);
+      float pbt = p[0] * va.x;
+      pbt = __builtin_fmaf(p[1], va.y, pbt);
+      pbt = __builtin_fmaf(p[2], va.z, pbt);
+      pbt = __builtin_fmaf(p[3], va.w, pbt);
+      pbt = __builtin_fmaf(p[4], vc.x, pbt);
+      pbt = __builtin_fmaf(p[5], vc.y, pbt);
+      pbt = __builtin_fmaf(p[6], vc.z, pbt);
+      pbt = __builtin_fmaf(p[7], vc.w, pbt);
+      pb_run = __builtin_fmaf(pb_run, alpha, pbt);
     }
-    uint32_t aw[4];
-    float spt = 0.f, pbt = 0.f;
-#pragma unroll
-    for (int pr = 0; pr < 4; pr++) {
-      const float x0 = Conv<T>::round(p[2 * pr] * vscale[2 * pr]);
-      const float x1 = Conv<T>::round(p[2 * pr + 1] * vscale[2 * pr + 1]);
-      aw[pr] = Mma<T>::pack2(x0, x1);
-      spt += x0 + x1;
-      pbt += p[2 * pr] * vbias[2 * pr] + p[2 * pr + 1] * vbias[2 * pr + 1];
-    }
-    sp_run = sp_run * alpha + spt;
-    pb_run = pb_run * alpha + pbt;
-    const u32x4_t aop = {aw[0], aw[1], aw[2], aw[3]};
 
-    // rescale the accumulator rows (4lg + i) by their head's alpha
-    if (__any(alpha != 1.0f)) {
+    // rescale the accumulator rows (4lg + i) by their head's alpha (the
+    // first tile skips this: the accumulators are still zero)
+    if (__any(alpha != 1.0f && m_old != -INFINITY)) {
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const float ai = __shfl(alpha, 4 * lg + i);
+        spacc[i] *= ai;
 #pragma unroll
         for (int tt = 0; tt < DT; tt++) oacc[tt][i] *= ai;
       }
     }
+    if constexpr (OFF != 0.0f) spacc = Mma<T>::mma(aop, ones, spacc);
 
     // value MFMAs: tile (m, e') covers d = (16m + ln) * E + e'
 #pragma unroll
     for (int m = 0; m < VM; m++) {
       if constexpr (BITS == 4) {
-        uint32_t plo[4], phi[4];
+        uint32_t pv[2][4];  // [lo/hi halves][key pair]
 #pragma unroll
         for (int pr = 0; pr < 4; pr++) {
-          plo[pr] = perm_b32(vreg[t][2 * pr + 1][m], vreg[t][2 * pr][m], 0x05040100u);
-          phi[pr] = perm_b32(vreg[t][2 * pr + 1][m], vreg[t][2 * pr][m], 0x07060302u);
+          pv[0][pr] = perm_b32(vb[2 * pr + 1][m], vb[2 * pr][m], 0x05040100u);
+          pv[1][pr] = perm_b32(vb[2 * pr + 1][m], vb[2 * pr][m], 0x07060302u);
         }
 #pragma unroll
         for (int ep = 0; ep < 8; ep++) {
           const int sh = 4 * (ep & 3);
-          u32x4_t bop;
-          bop.x = (((ep < 4 ? plo[0] : phi[0]) >> sh) & 0x000f000fu) | Mma<T>::MAGIC;
-          bop.y = (((ep < 4 ? plo[1] : phi[1]) >> sh) & 0x000f000fu) | Mma<T>::MAGIC;
-          bop.z = (((ep < 4 ? plo[2] : phi[2]) >> sh) & 0x000f000fu) | Mma<T>::MAGIC;
-          bop.w = (((ep < 4 ? plo[3] : phi[3]) >> sh) & 0x000f000fu) | Mma<T>::MAGIC;
+          const uint32_t* src = pv[ep >> 2];
+          const u32x4_t bop = {bfi32(0x000f000fu, src[0] >> sh, magic), bfi32(0x000f000fu, src[1] >> sh, magic),
+                               bfi32(0x000f000fu, src[2] >> sh, magic), bfi32(0x000f000fu, src[3] >> sh, magic)};
           oacc[m * E + ep] = Mma<T>::mma(aop, bop, oacc[m * E + ep]);
         }
       } else {
@@ -334,7 +472,7 @@ __global__ void __launch_bounds__(256) sdpa_decode_mfma_kernel(
           uint32_t bw[4];
 #pragma unroll
           for (int pr = 0; pr < 4; pr++) {
-            const uint32_t wa = vreg[t][2 * pr][m], wb = vreg[t][2 * pr + 1][m];
+            const uint32_t wa = vb[2 * pr][m], wb = vb[2 * pr + 1][m];
             if constexpr (std::is_same<T, BF16>::value) {
               const float fa = (float)((wa >> (8 * ep)) & 0xffu);
               const float fb = (float)((wb >> (8 * ep)) & 0xffu);
@@ -349,98 +487,133 @@ __global__ void __launch_bounds__(256) sdpa_decode_mfma_kernel(
         }
       }
     }
+  };
+
+  // ---- stream the wave's tiles through the two-slot window ----------------
+#pragma unroll
+  for (int t = 0; t < TPW; t++) {
+    if ((wave_u + NW * t) * 32 < nk) compute(t, kbuf[t % WIN], vbuf[t % WIN]);  // wave-uniform
+    __builtin_amdgcn_sched_barrier(0);
+    if (t + WIN < TPW) issue(t + WIN, kbuf[t % WIN], vbuf[t % WIN]);
+    __builtin_amdgcn_sched_barrier(0);
   }
 
-  // ---- wave result: u[h][d] = O - off * sp + pb (rows whose group owns d) -
-  l_run += __shfl_xor(l_run, 16);
-  l_run += __shfl_xor(l_run, 32);
-  sp_run += __shfl_xor(sp_run, 16);
-  sp_run += __shfl_xor(sp_run, 32);
-  pb_run += __shfl_xor(pb_run, 16);
-  pb_run += __shfl_xor(pb_run, 32);
-  constexpr float VOFF = CodeOps<T, BITS>::OFFSET;
+  // ---- wave result: u[h][d] = O - OFF * sp + pb (rows whose group owns d) -
+  l_run = xrow_sum(l_run);
+  pb_run = xrow_sum(pb_run);
+  __syncthreads();  // every wave is done reading sb_lds, which u_lds overlays
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const int r = 4 * lg + i;
-    const float sp_r = __shfl(sp_run, r);
     const float pb_r = __shfl(pb_run, r);
     if (r < R) {
-      const int g = r / nrep, h = r % nrep;
+      const int g = r % G, h = r / G;
+      const float corr = pb_r - OFF * spacc[i];
 #pragma unroll
       for (int tt = 0; tt < DT; tt++) {
         const int m = tt / E, ep = tt % E;
         const int d = (16 * m + ln) * E + ep;
-        if (d / GS == g) u_lds[wave][h * D + d] = oacc[tt][i] - VOFF * sp_r + pb_r;
+        if (d / GS == g) u_lds[wave][h * D + d] = oacc[tt][i] + corr;
       }
     }
   }
-  if (lane < nrep) {
-    m_lds[wave][lane] = m_run;  // lane < nrep has h_me = lane (group 0)
-    l_lds[wave][lane] = l_run;
+  if (lane < R && g_me == 0) {
+    m_lds[wave][h_me] = m_run;
+    l_lds[wave][h_me] = l_run;
   }
   __syncthreads();
 
-  // ---- merge the four waves ----------------------------------------------
-  const bool single = nch == 1;
-  const int64_t pstride = (int64_t)nrep * (D + 2);
-  float* mypart = part + (((int64_t)b * Hkv + kvh) * gridDim.x + c) * pstride;
-  for (int idx = tid; idx < nrep * D; idx += 256) {
-    const int h = idx / D, d = idx % D;
+  // ---- merge the waves (fixed order) ---------------------------------------
+  const bool single = cr.nch == 1;
+  const int64_t bk = (int64_t)b * Hkv + kvh;
+  const int nd = nrep * D;
+  const int64_t pc = bk * gridDim.x + c;  // this chunk's partial slot
+  for (int idx = tid; idx < nd; idx += NT) {
+    const int h = idx / D;
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < 4; w++) M = fmaxf(M, m_lds[w][h]);
+    for (int w = 0; w < NW; w++) M = fmaxf(M, m_lds[w][h]);
     float U = 0.f, L = 0.f;
 #pragma unroll
-    for (int w = 0; w < 4; w++) {
-      const float f = exp2f(m_lds[w][h] - M);  // empty wave: m = -inf -> 0
-      if (f > 0.f) {
-        U += f * u_lds[w][idx];
-        L += f * l_lds[w][h];
-      }
+    for (int w = 0; w < NW; w++) {
+      const float f = __builtin_amdgcn_exp2f(m_lds[w][h] - M);  // idle wave: m = -inf -> 0
+      U = __builtin_fmaf(f, u_lds[w][idx], U);
+      L = __builtin_fmaf(f, l_lds[w][h], L);
     }
     if (single) {
       Conv<T>::store(out, out_base + idx, U / L);
     } else {
-      mypart[h * (D + 2) + d] = U;
-      if (d == 0) {
-        mypart[h * (D + 2) + D] = M;
-        mypart[h * (D + 2) + D + 1] = L;
-      }
+      part_o[pc * nd + idx] = U;
+      if (idx % D == 0) part_ml[pc * nrep + h] = make_float2(M, L);
     }
   }
-  if (single) return;
+}
 
-  // ---- last chunk to arrive merges all chunks of this (b, kv head) -------
-  // One release RMW per workgroup publishes its partial (the barrier makes
-  // every thread's stores part of thread 0's release); only the merging
-  // workgroup pays the acquire.  No full fence: that would invalidate the L2
-  // under every other workgroup still streaming K/V.
-  __syncthreads();
-  if (tid == 0) {
-    uint32_t* ctr = counters + (int64_t)b * Hkv + kvh;
-    const uint32_t prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-    last_flag = prev == (uint32_t)(nch - 1);
-    if (last_flag) {
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-      __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+// Split-K merge: out[b, kvh*nrep + h, d] = sum_c U_c e^{M_c - M} / sum_c L_c e^{M_c - M}
+// over the chunks c of row b (the reference's deterministic flash-decoding
+// merge, src/model/fused-decode-kernel.ts:205-222).  Workgroup (cb, kvh, b)
+// owns 64 float4 columns of (h, d); its four waves fold the chunks
+// c = wave, wave + 4, ... with an online merge and combine in LDS in fixed
+// order.  Rows whose keys fit one chunk were finished by the partial kernel.
+template <typename T>
+__global__ void __launch_bounds__(256) sdpa_decode_merge_kernel(const float4* __restrict__ part_o,
+                                                                const float2* __restrict__ part_ml, int Hq, int Hkv,
+                                                                int D, Geometry geo, int chunk, int nslots,
+                                                                uint16_t* __restrict__ out) {
+  __shared__ float4 ul[4][64];
+  __shared__ float2 mll[4][64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int b = blockIdx.z, kvh = blockIdx.y;
+  const int nrep = Hq / Hkv;
+  const int cols = nrep * D / 4;
+  const int col = blockIdx.x * 64 + lane;
+  const int nch = chunk_range(geo, b, chunk, 0).nch;
+  if (nch <= 1) return;
+  const int64_t bk = (int64_t)b * Hkv + kvh;
+  const bool active = col < cols;
+  const int colc = active ? col : cols - 1;
+  const int h = (colc * 4) / D;
+  const float4* po = part_o + bk * nslots * cols;
+  const float2* pml = part_ml + bk * nslots * nrep;
+  float M = -INFINITY, L = 0.f;
+  float4 U = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 8
+  for (int cc = wave; cc < nch; cc += 4) {
+    const float2 ml = pml[cc * nrep + h];
+    const float4 u = po[(int64_t)cc * cols + colc];
+    const float Mn = fmaxf(M, ml.x);
+    const float a = __builtin_amdgcn_exp2f(M - Mn), f = __builtin_amdgcn_exp2f(ml.x - Mn);  // M = -inf -> a = 0
+    L = L * a + ml.y * f;
+    U.x = U.x * a + u.x * f;
+    U.y = U.y * a + u.y * f;
+    U.z = U.z * a + u.z * f;
+    U.w = U.w * a + u.w * f;
+    M = Mn;
   }
+  ul[wave][lane] = U;
+  mll[wave][lane] = make_float2(M, L);
   __syncthreads();
-  if (!last_flag) return;
-  const float* parts = part + ((int64_t)b * Hkv + kvh) * gridDim.x * pstride;
-  for (int idx = tid; idx < nrep * D; idx += 256) {
-    const int h = idx / D, d = idx % D;
-    float M = -INFINITY;
-    for (int cc = 0; cc < nch; cc++) M = fmaxf(M, parts[cc * pstride + h * (D + 2) + D]);
-    float U = 0.f, L = 0.f;
-    for (int cc = 0; cc < nch; cc++) {
-      const float* pc = parts + cc * pstride + h * (D + 2);
-      const float f = exp2f(pc[D] - M);
-      U += f * pc[d];
-      L += f * pc[D + 1];
-    }
-    Conv<T>::store(out, out_base + idx, U / L);
+  if (wave != 0 || !active) return;
+  float Mt = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < 4; w++) Mt = fmaxf(Mt, mll[w][lane].x);
+  float Lt = 0.f;
+  float4 Ut = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int w = 0; w < 4; w++) {
+    const float f = __builtin_amdgcn_exp2f(mll[w][lane].x - Mt);  // wave with no chunk: -inf -> 0
+    const float4 u = ul[w][lane];
+    Lt = __builtin_fmaf(f, mll[w][lane].y, Lt);
+    Ut.x = __builtin_fmaf(f, u.x, Ut.x);
+    Ut.y = __builtin_fmaf(f, u.y, Ut.y);
+    Ut.z = __builtin_fmaf(f, u.z, Ut.z);
+    Ut.w = __builtin_fmaf(f, u.w, Ut.w);
   }
+  const int64_t o = ((int64_t)b * Hq + (int64_t)kvh * nrep) * D + (int64_t)col * 4;
+  Conv<T>::store(out, o, Ut.x / Lt);
+  Conv<T>::store(out, o + 1, Ut.y / Lt);
+  Conv<T>::store(out, o + 2, Ut.z / Lt);
+  Conv<T>::store(out, o + 3, Ut.w / Lt);
 }
 
 // ========================================================== generic kernel
@@ -550,31 +723,59 @@ __global__ void __launch_bounds__(128) sdpa_generic_kernel(
   }
 }
 
+// Keys per workgroup: MLXQ_DECODE_CHUNK (a power of two in [32, MAXC]) if
+// set, else the largest chunk that still gives every CU a workgroup.
+int decode_chunk_override() {
+  static const int v = [] {
+    const char* e = getenv("MLXQ_DECODE_CHUNK");
+    return e ? atoi(e) : 0;
+  }();
+  return v;
+}
+
 template <typename T, int BITS, int D, int GS>
 int launch_decode(const void* q, int B, int Hq, int Hkv, const uint32_t* kp, const void* ks, const void* kb,
                   const uint32_t* vp, const void* vs, const void* vb, Geometry geo, float scale, void* out,
                   hipStream_t s) {
-  constexpr int TPW = D <= 128 ? 4 : 2;
-  constexpr int MAXC = 128 * TPW;
+  using SH = DecodeShape<BITS, D, GS>;
+  constexpr int MAXC = SH::MAXC;
+  MLXQ_CHECK(geo.cap * (int64_t)SH::KW * 4 < ((int64_t)1 << 31), "kv cache rows too long for one launch");
   const int64_t span = geo.valid_len ? geo.cap : geo.n_kv;  // per-row upper bound on keys
-  // aim for ~4 workgroups per CU over the whole launch
-  const int64_t target = (int64_t)mlxq::device_cu_count() * 4;
-  int64_t want = (span * B * Hkv + target - 1) / target;
-  int chunk = 128;
-  while (chunk < MAXC && chunk < want) chunk *= 2;
-  const int64_t nchunks = span > 0 ? (span + chunk - 1) / chunk : 1;
+  int chunk = MAXC;
+  const int ov = decode_chunk_override();
+  if (ov >= 32 && ov <= MAXC && (ov & (ov - 1)) == 0) {
+    chunk = ov;
+  } else {
+    const int64_t cus = mlxq::device_cu_count();
+    while (chunk > 128 && ((span + chunk - 1) / chunk) * B * Hkv < cus) chunk /= 2;
+  }
+  // a ring row's window may start mid-chunk at the wrap point: one extra chunk
+  const int64_t nchunks = (span > 0 ? (span + chunk - 1) / chunk : 1) + (geo.ring_off ? 1 : 0);
   MLXQ_CHECK(nchunks < 65536, "kv length too large for one launch");
-  uint32_t* counters = nullptr;
   void* pws = nullptr;
   const int nrep = Hq / Hkv;
-  const size_t pbytes = (size_t)B * Hkv * nchunks * nrep * (D + 2) * sizeof(float);
-  int rc = mlxq::workspace(pbytes, (size_t)B * Hkv, &counters, &pws, s);
-  if (rc) return rc;
+  const size_t slots = (size_t)B * Hkv * nchunks;
+  const size_t obytes = (slots * nrep * D * sizeof(float) + 255) & ~(size_t)255;
+  const size_t pbytes = nchunks > 1 ? obytes + slots * nrep * sizeof(float2) : 0;
+  if (pbytes) {
+    uint32_t* unused_counters = nullptr;
+    int rc = mlxq::workspace(pbytes, 0, &unused_counters, &pws, s);
+    if (rc) return rc;
+  }
+  float* part_o = (float*)pws;
+  float2* part_ml = pbytes ? (float2*)((uint8_t*)pws + obytes) : nullptr;
   dim3 grid((unsigned)nchunks, (unsigned)Hkv, (unsigned)B);
-  hipLaunchKernelGGL((sdpa_decode_mfma_kernel<T, BITS, D, GS, TPW>), grid, dim3(256), 0, s, (const uint16_t*)q, kp,
-                     (const uint16_t*)ks, (const uint16_t*)kb, vp, (const uint16_t*)vs, (const uint16_t*)vb, Hq,
-                     Hkv, geo, scale, chunk, (uint16_t*)out, (float*)pws, counters);
+  hipLaunchKernelGGL((sdpa_decode_mfma_kernel<T, BITS, D, GS>), grid, dim3(SH::NW * 64), 0, s, (const uint16_t*)q,
+                     kp, (const uint16_t*)ks, (const uint16_t*)kb, vp, (const uint16_t*)vs, (const uint16_t*)vb, Hq,
+                     Hkv, geo, scale, chunk, (uint16_t*)out, part_o, part_ml);
   MLXQ_LAUNCHED("sdpa_decode_mfma_kernel");
+  if (nchunks > 1) {
+    const int cols = nrep * D / 4;
+    dim3 mgrid((unsigned)((cols + 63) / 64), (unsigned)Hkv, (unsigned)B);
+    hipLaunchKernelGGL((sdpa_decode_merge_kernel<T>), mgrid, dim3(256), 0, s, (const float4*)part_o, part_ml, Hq,
+                       Hkv, D, geo, chunk, (int)nchunks, (uint16_t*)out);
+    MLXQ_LAUNCHED("sdpa_decode_merge_kernel");
+  }
   return MLXQ_OK;
 }
 
@@ -594,11 +795,15 @@ int launch_decode_d(int D, int gs, const void* q, int B, int Hq, int Hkv, const 
   return mlxq::fail(MLXQ_ERR_UNSUPPORTED, "decode: no MFMA instance for this head_dim/group_size");
 }
 
-bool decode_mfma_ok(int dtype, int bits, int D, int gs, int nrep) {
+// The MFMA decode kernel reads a cache row's G = D/gs scales (biases) with
+// one 2G-byte load, so those arrays must be 2G-byte aligned.
+bool decode_mfma_ok(int dtype, int bits, int D, int gs, int nrep, std::initializer_list<const void*> sb) {
   if (!mlxq::is_half_dtype(dtype)) return false;
   if (bits != 4 && bits != 8) return false;
   const bool dok = D == 128 || D == 256 || (bits == 8 && D == 64 && gs <= 64);
   if (!dok) return false;
+  for (const void* p : sb)
+    if ((uintptr_t)p % (2 * (D / gs))) return false;
   return nrep * (D / gs) <= 16;
 }
 
@@ -631,7 +836,7 @@ extern "C" int mlxq_quantized_sdpa(const void* q, int dtype, int B, int Hq, int 
   const int nrep = Hq / Hkv;
   // Lq = 1 attends every valid key under either mask (its position is the last one)
   const bool decode = Lq == 1 && (mask_mode == MLXQ_MASK_NONE || window == 0);
-  if (decode && decode_mfma_ok(dtype, bits, D, group_size, nrep)) {
+  if (decode && decode_mfma_ok(dtype, bits, D, group_size, nrep, {k_scales, k_biases, v_scales, v_biases})) {
     if (dtype == MLXQ_BFLOAT16)
       return bits == 4 ? launch_decode_d<BF16, 4>(D, group_size, q, B, Hq, Hkv, k_packed, k_scales, k_biases,
                                                   v_packed, v_scales, v_biases, geo, scale, out, s)
