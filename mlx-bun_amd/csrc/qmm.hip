@@ -1,171 +1,244 @@
 // qmm.hip -- mx.quantized_matmul for MLX affine-quantized weights (gfx950).
 //
-// Main path (transpose = true, bits in {4, 8}, group 64/128, T = bf16/f16):
-// the weight stream is the roofline, so codes never leave registers as
-// anything but exact MFMA operands.  Per 64-k tile (one quantization group
-// for gs = 64) each lane loads the 16 codes of one weight row it owns, turns
-// them into two k-steps of a v_mfma_f32_16x16x32 B operand by the
-// mantissa-OR trick (mfma_common.h), and the group's
-//     y += s * sum_k x_k (c_k + off)  +  (b - off * s) * sum_k x_k
-// is applied to the 16x16 accumulator once per group.  sum_k x_k comes from a
-// second MFMA against a ones operand, so no VALU work depends on M.
-// x operands are read from global memory (L1/L2 resident; identical
-// addresses across lanes when M is small) and permuted into the codes' slot
-// order in registers.  Work: a workgroup = 16 weight rows; its waves split K
-// and reduce in LDS (deterministic, no cross-workgroup traffic).
+// qmv path (transpose = true, M small, bits in {4, 8}, group 64/128,
+// T = bf16/f16): the weight stream is the roofline.  A weight tile is 16 rows
+// x one 64-byte segment of each row (128 codes at 4 bits, 64 at 8); lane
+// (n = l%16, q = l/16) holds 16 contiguous bytes of row n, which become the B
+// operand of v_mfma_f32_16x16x32 by the mantissa-OR trick (codes stay exact;
+// mfma_common.h).  A k-step takes 8 codes from each lane quarter, so when a
+// tile holds QG > 1 quantization groups the MFMA rows are indexed by
+// (activation row m, group qg): row (m, qg) carries x[m] only in the lane
+// quarters of group qg and zeros elsewhere, and every row's dot stays inside
+// one group.  Per tile the 16x16 accumulator gets
+//     y[m, n] += s[n, g] * D[(m, g), n] + (b[n, g] - off * s[n, g]) * X[(m, g)]
+// where X is the same A operand against a ones operand (sum of x over the
+// group).  x is staged once per workgroup in LDS, pre-permuted into the code
+// slot order, so per-tile waits only ever cover the weight stream (vector
+// loads complete in order, LDS reads have their own counter).
+// A workgroup owns 16 R weight rows and all of K; its NW waves take TPW
+// consecutive tiles each, issue every weight/scale/bias load of those tiles
+// up front (raw buffer loads: rows past N and scales past the row read 0
+// without a branch) and reduce their partial rows in LDS (fixed order, no
+// cross-workgroup traffic).
 //
 // Everything else (transpose = false, 2-bit, group 32, fp32 activations,
-// odd shapes) takes a straightforward VALU kernel.
+// larger M) takes the dequantize-to-LDS MFMA kernel or the VALU kernel below.
+#include <cstdlib>
+
 #include "mfma_common.h"
 
 namespace {
 
-constexpr int QMV_CT = 8;  // tiles per register chunk (double-buffered)
+// weight tiles each qmv wave keeps in flight
+#ifndef QMV_WIN
+#define QMV_WIN 2
+#endif
 
-// Load one chunk of QMV_CT 64-k tiles of this lane's weight row (16 codes per
-// tile) plus their scales/biases.
-template <typename T, int BITS, int GS>
-__device__ __forceinline__ void qmv_load_chunk(const uint32_t* __restrict__ wrow_ptr, const uint16_t* __restrict__ srow,
-                                               const uint16_t* __restrict__ brow, int tile0, int tile_end, int lg,
-                                               uint32_t (&wreg)[QMV_CT][BITS / 2], float (&sreg)[QMV_CT],
-                                               float (&breg)[QMV_CT]) {
-  constexpr int WPT = BITS / 2;
-#pragma unroll
-  for (int t = 0; t < QMV_CT; t++) {
-    const int tile = tile0 + t;
-    if (tile < tile_end) {
-      const uint32_t* src = wrow_ptr + ((int64_t)tile * 64 + lg * 16) * BITS / 32;
-      if constexpr (WPT == 2) {
-        const uint2 v = *reinterpret_cast<const uint2*>(src);
-        wreg[t][0] = v.x;
-        wreg[t][WPT - 1] = v.y;
-      } else {
-        const uint4 v = *reinterpret_cast<const uint4*>(src);
-        wreg[t][0] = v.x;
-        wreg[t][1 % WPT] = v.y;
-        wreg[t][2 % WPT] = v.z;
-        wreg[t][3 % WPT] = v.w;
-      }
-      sreg[t] = Conv<T>::from_bits(srow[(int64_t)tile * 64 / GS]);
-      breg[t] = Conv<T>::from_bits(brow[(int64_t)tile * 64 / GS]);
-    }
-  }
-}
-
-template <typename T, int BITS, int GS, int MB>
-__device__ __forceinline__ void qmv_compute_chunk(const uint16_t* __restrict__ x, int64_t M, int64_t K, int tile0,
-                                                  int tile_end, int ln, int lg,
-                                                  const uint32_t (&wreg)[QMV_CT][BITS / 2],
-                                                  const float (&sreg)[QMV_CT], const float (&breg)[QMV_CT],
-                                                  f32x4_t (&yacc)[MB]) {
+template <typename T, int BITS, int GS, int MB, int R, int TPW, int MR>
+__global__ void __launch_bounds__(512) qmv_kernel(const uint16_t* __restrict__ x, int M, int K,
+                                                  const uint32_t* __restrict__ w,
+                                                  const uint16_t* __restrict__ scales,
+                                                  const uint16_t* __restrict__ biases, int N, int w_rep,
+                                                  uint16_t* __restrict__ y) {
   using CO = CodeOps<T, BITS>;
-  constexpr int WPT = BITS / 2;
+  constexpr int TILE_K = 512 / BITS;                 // codes per 64-byte row segment
+  constexpr int KS = TILE_K / 32;                    // MFMA k-steps per tile
+  constexpr int QG = TILE_K > GS ? TILE_K / GS : 1;  // quantization groups per tile (1 or 2)
+  constexpr int NGW = TPW * TILE_K / GS;             // groups per wave (a multiple of 4)
+  constexpr int SCH = 16 * R * NGW / 4;              // 8-byte scale chunks per wave
+  constexpr int SPL = (SCH + 63) / 64;               // ... per lane
+  constexpr int XPW = TPW * TILE_K;                  // x values per row per wave
+  constexpr int XC = 8;                              // x chunks (8 values) per lane, at most
+  constexpr float OFF = CO::OFFSET;
+  static_assert(QG <= 2 && NGW % 4 == 0, "tile / group geometry");
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int tid = threadIdx.x, lane = tid & 63, nw = blockDim.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar offsets need it
+  const int ln = lane & 15, lq = lane >> 4;
+  const int bidx = blockIdx.y, wb = bidx / w_rep;
+  const int n0 = blockIdx.x * 16 * R;
+  const int rows = min(16 * R, N - n0);
+  const int G = K / GS, KT = K / TILE_K;
+  const uint32_t row_bytes = (uint32_t)K * BITS / 8;
+  x += (int64_t)bidx * M * K;
+  y += (int64_t)bidx * M * N;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (uint32_t)(M * K * 2));
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(w + ((int64_t)wb * N + n0) * (row_bytes / 4), (uint32_t)rows * row_bytes);
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(scales + ((int64_t)wb * N + n0) * G, (uint32_t)(rows * G * 2));
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(biases + ((int64_t)wb * N + n0) * G, (uint32_t)(rows * G * 2));
+  // This wave's tiles [t_first, t_first + TPW) (the last wave's tail tiles
+  // are clamped duplicates that add nothing) and its private LDS region:
+  // x slice [M + 1][XPW] in code-slot order (row M all zero: the A operand
+  // of lanes whose group or row is inactive), then (s, b - off s) as float2
+  // [NGW][16R].
+  const int t_first = wave * TPW;
+  const int k_first = t_first * TILE_K, g_first = k_first / GS;
+  const int xchunks = M * XPW / 8;
+  const size_t wave_lds = (size_t)(M + 1) * XPW * 2 + (size_t)NGW * 16 * R * 8;
+  uint16_t* xl = reinterpret_cast<uint16_t*>(smem + wave * wave_lds);
+  float2* sbl = reinterpret_cast<float2*>(smem + wave * wave_lds + (size_t)(M + 1) * XPW * 2);
+
+  // ---- 1. x slice and scales/biases of this wave (coalesced), issued before
+  // the weight stream: vector loads complete in order, so waiting for these
+  // never waits for weights ---------------------------------------------------
+  u32x4_t xst[XC];
+#pragma unroll
+  for (int c = 0; c < XC; c++) {
+    const int ci = lane + 64 * c;  // chunk ci: row ci / (XPW/8), 8 values
+    const int m = ci / (XPW / 8), kk = k_first + 8 * (ci % (XPW / 8));
+    const uint32_t off = (ci < xchunks && kk < K) ? (uint32_t)(m * K + kk) * 2u : 0x80000000u;
+    xst[c] = buf_load128(rx, off, 0u);
+  }
+  uint32_t sst[SPL][2], bst[SPL][2];
+#pragma unroll
+  for (int c = 0; c < SPL; c++) {
+    const int ci = lane + 64 * c;  // chunk ci: row ci % 16R, groups g_first + 4 (ci / 16R) ..
+    const int r = ci % (16 * R), g4 = g_first + 4 * (ci / (16 * R));
+    const uint32_t off = (ci < SCH && g4 < G) ? (uint32_t)(r * G + g4) * 2u : 0x80000000u;
+    const auto sv = __builtin_amdgcn_raw_buffer_load_b64(rs, (int)off, 0, 0);
+    const auto bv = __builtin_amdgcn_raw_buffer_load_b64(rb, (int)off, 0, 0);
+    sst[c][0] = sv[0];
+    sst[c][1] = sv[1];
+    bst[c][0] = bv[0];
+    bst[c][1] = bv[1];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- 2. the weight stream: the first QMV_WIN tiles of this wave ----------
+  u32x4_t wr[TPW][R];
+  // rows past N sit past the descriptor's end and read 0; the tile offset
+  // (inside the row) rides in the scalar offset
+  uint32_t wlane[R];
+#pragma unroll
+  for (int ri = 0; ri < R; ri++) wlane[ri] = (uint32_t)(ln + 16 * ri) * row_bytes + 16u * lq;
+  auto issue = [&](int t) {
+    const uint32_t toff = (uint32_t)min(t_first + t, KT - 1) * 64u;
+#pragma unroll
+    for (int ri = 0; ri < R; ri++) wr[t][ri] = buf_load128(rw, wlane[ri], toff);
+  };
+#pragma unroll
+  for (int t = 0; t < QMV_WIN && t < TPW; t++) issue(t);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- 3. this wave's LDS region (no workgroup barrier) -------------------
+#pragma unroll
+  for (int c = 0; c < XC; c++) {
+    if (64 * c < xchunks) {  // uniform
+      const int ci = lane + 64 * c;
+      if (ci < xchunks) *reinterpret_cast<u32x4_t*>(xl + ci * 8) = permute8<CO::ORDER>(xst[c]);
+    }
+  }
+  for (int c = lane; c < XPW / 8; c += 64) *reinterpret_cast<u32x4_t*>(xl + M * XPW + 8 * c) = u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int c = 0; c < SPL; c++) {
+    const int ci = lane + 64 * c;
+    if (ci < SCH) {
+      const int r = ci % (16 * R), gl = 4 * (ci / (16 * R));
+#pragma unroll
+      for (int p = 0; p < 2; p++) {
+        const float s0 = Conv<T>::from_bits(sst[c][p] & 0xffffu), s1 = Conv<T>::from_bits(sst[c][p] >> 16);
+        const float b0 = Conv<T>::from_bits(bst[c][p] & 0xffffu), b1 = Conv<T>::from_bits(bst[c][p] >> 16);
+        sbl[(gl + 2 * p) * 16 * R + r] = make_float2(s0, b0 - OFF * s0);
+        sbl[(gl + 2 * p + 1) * 16 * R + r] = make_float2(s1, b1 - OFF * s1);
+      }
+    }
+  }
+  // (a wave reads back its own LDS writes in order: no barrier needed)
+
+  // A-operand rows: r = ln + 16 rb = (m, qg); lane quarter lq belongs to group
+  // lq * QG / 4 of the tile
+  const uint16_t* xa[MB];
+#pragma unroll
+  for (int rb = 0; rb < MB; rb++) {
+    const int r = ln + 16 * rb, m = r / QG, qg = r % QG;
+    xa[rb] = xl + ((lq * QG / 4 == qg && m < M) ? m : M) * XPW + lq * (TILE_K / 4);
+  }
   const u32x4_t ones = {Mma<T>::ONES, Mma<T>::ONES, Mma<T>::ONES, Mma<T>::ONES};
+  const uint32_t magic = opaque(Mma<T>::MAGIC);
+  f32x4_t yacc[R][MB];
 #pragma unroll
-  for (int t = 0; t < QMV_CT; t++) {
-    const int tile = tile0 + t;
-    if (tile < tile_end) {
-      u32x4_t b0, b1;
-      if constexpr (BITS == 4) {
-        b0 = CodeOps<T, 4>::operand(wreg[t][0]);
-        b1 = CodeOps<T, 4>::operand(wreg[t][WPT - 1]);
-      } else {
-        b0 = CodeOps<T, BITS>::operand(wreg[t][0], wreg[t][1 % WPT]);
-        b1 = CodeOps<T, BITS>::operand(wreg[t][2 % WPT], wreg[t][3 % WPT]);
-      }
-      const float sc = sreg[t];
-      const float bb = breg[t] - CO::OFFSET * sc;
-      const int64_t k = (int64_t)tile * 64 + lg * 16;
+  for (int ri = 0; ri < R; ri++)
 #pragma unroll
-      for (int rb = 0; rb < MB; rb++) {
-        int64_t m = rb * 16 + ln;
-        m = m < M ? m : M - 1;
-        const uint16_t* xr = x + m * K + k;
-        const u32x4_t a0 = permute8<CO::ORDER>(*reinterpret_cast<const u32x4_t*>(xr));
-        const u32x4_t a1 = permute8<CO::ORDER>(*reinterpret_cast<const u32x4_t*>(xr + 8));
-        // D = x (A, rows m) . codes (B, cols n); the ones operand gives sum x
-        f32x4_t acc = Mma<T>::mma(a0, b0, f32x4_t{0.f, 0.f, 0.f, 0.f});
-        acc = Mma<T>::mma(a1, b1, acc);
-        f32x4_t xs = Mma<T>::mma(a0, ones, f32x4_t{0.f, 0.f, 0.f, 0.f});
-        xs = Mma<T>::mma(a1, ones, xs);
+    for (int rb = 0; rb < MB; rb++) yacc[ri][rb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  // ---- 4. tiles: compute tile t, then request tile t + QMV_WIN --------------
+  // (a clamped duplicate tail tile reads zero x and zero scales: adds nothing)
 #pragma unroll
-        for (int i = 0; i < 4; i++) yacc[rb][i] += sc * acc[i] + bb * xs[i];
-      }
-    }
-  }
-}
-
-// One workgroup = 16 weight rows (MFMA columns); its NW waves split the K
-// axis into contiguous tile ranges and their partial sums meet in LDS.  No
-// cross-workgroup traffic.  Weight codes are double-buffered in registers
-// by chunks of QMV_CT tiles so the next chunk's loads are in flight while
-// the current one computes.
-template <typename T, int BITS, int GS, int MB, int NW>
-__global__ void __launch_bounds__(NW * 64) qmv_mfma_kernel(const uint16_t* __restrict__ x, int64_t M, int64_t K,
-                                                            const uint32_t* __restrict__ w,
-                                                            const uint16_t* __restrict__ scales,
-                                                            const uint16_t* __restrict__ biases, int64_t N,
-                                                            int64_t w_rep, uint16_t* __restrict__ y) {
-  constexpr int WPT = BITS / 2;
-  __shared__ f32x4_t red[NW][MB][64];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int ln = lane & 15, lg = lane >> 4;
-  const int64_t bidx = blockIdx.y;
-  const int64_t wb = bidx / w_rep;
-  x += bidx * M * K;
-  y += bidx * M * N;
-  w += wb * N * (K * BITS / 32);
-  scales += wb * N * (K / GS);
-  biases += wb * N * (K / GS);
-
-  const int64_t n = (int64_t)blockIdx.x * 16 + ln;
-  const int64_t nl = n < N ? n : N - 1;  // clamp loads; stores are masked
-  const int tiles = (int)(K / 64);
-  const int per = (tiles + NW - 1) / NW;
-  const int t_begin = min(tiles, wave * per);
-  const int t_end = min(tiles, t_begin + per);
-  const uint32_t* wrow_ptr = w + nl * (K * BITS / 32);
-  const uint16_t* srow = scales + nl * (K / GS);
-  const uint16_t* brow = biases + nl * (K / GS);
-
-  f32x4_t yacc[MB];
-#pragma unroll
-  for (int rb = 0; rb < MB; rb++) yacc[rb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-  uint32_t wa[QMV_CT][WPT], wbuf[QMV_CT][WPT];
-  float sa[QMV_CT], ba[QMV_CT], sb2[QMV_CT], bb2[QMV_CT];
-  qmv_load_chunk<T, BITS, GS>(wrow_ptr, srow, brow, t_begin, t_end, lg, wa, sa, ba);
-  for (int c0 = t_begin; c0 < t_end; c0 += 2 * QMV_CT) {
-    const int c1 = c0 + QMV_CT;
-    if (c1 < t_end) qmv_load_chunk<T, BITS, GS>(wrow_ptr, srow, brow, c1, t_end, lg, wbuf, sb2, bb2);
-    qmv_compute_chunk<T, BITS, GS, MB>(x, M, K, c0, t_end, ln, lg, wa, sa, ba, yacc);
-    if (c1 < t_end) {
-      if (c1 + QMV_CT < t_end) qmv_load_chunk<T, BITS, GS>(wrow_ptr, srow, brow, c1 + QMV_CT, t_end, lg, wa, sa, ba);
-      qmv_compute_chunk<T, BITS, GS, MB>(x, M, K, c1, t_end, ln, lg, wbuf, sb2, bb2, yacc);
-    }
-  }
-
-  // ---- reduce the NW waves' partials; D layout row = 4*lg + i, col = ln ---
-#pragma unroll
-  for (int rb = 0; rb < MB; rb++) red[wave][rb][lane] = yacc[rb];
-  __syncthreads();
-  if (wave == 0 && n < N) {
+  for (int t = 0; t < TPW; t++) {
+    f32x4_t D[R][MB], X[MB];
 #pragma unroll
     for (int rb = 0; rb < MB; rb++) {
-      f32x4_t acc = red[0][rb][lane];
+      X[rb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int wv = 1; wv < NW; wv++) {
-        const f32x4_t o = red[wv][rb][lane];
-        acc[0] += o[0];
-        acc[1] += o[1];
-        acc[2] += o[2];
-        acc[3] += o[3];
+      for (int ri = 0; ri < R; ri++) D[ri][rb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int j = 0; j < KS; j++) {
+      u32x4_t bop[R];
+#pragma unroll
+      for (int ri = 0; ri < R; ri++) {
+        const u32x4_t& wv = wr[t][ri];
+        if constexpr (BITS == 4)
+          bop[ri] = CodeOps<T, 4>::operand(wv[j], magic);
+        else
+          bop[ri] = CodeOps<T, BITS>::operand(wv[2 * j], wv[2 * j + 1]);
       }
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int64_t m = rb * 16 + lg * 4 + i;
-        if (m < M) y[m * N + n] = (uint16_t)Conv<T>::to_bits(acc[i]);
+      for (int rb = 0; rb < MB; rb++) {
+        const u32x4_t a = *reinterpret_cast<const u32x4_t*>(xa[rb] + t * TILE_K + 8 * j);
+        X[rb] = Mma<T>::mma(a, ones, X[rb]);
+#pragma unroll
+        for (int ri = 0; ri < R; ri++) D[ri][rb] = Mma<T>::mma(a, bop[ri], D[ri][rb]);
       }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (t + QMV_WIN < TPW) issue(t + QMV_WIN);
+    __builtin_amdgcn_sched_barrier(0);
+    const int gl = t * TILE_K / GS;
+#pragma unroll
+    for (int ri = 0; ri < R; ri++) {
+      float s[QG], bb[QG];
+#pragma unroll
+      for (int qg = 0; qg < QG; qg++) {
+        const float2 sb = sbl[(gl + qg) * 16 * R + ln + 16 * ri];
+        s[qg] = sb.x;
+        bb[qg] = sb.y;
+      }
+      // MR < 4: only rows 0 .. MR-1 (lane quarter 0) reach the output
+#pragma unroll
+      for (int rb = 0; rb < MB; rb++)
+#pragma unroll
+        for (int i = 0; i < MR; i++)
+          yacc[ri][rb][i] = __builtin_fmaf(s[i % QG], D[ri][rb][i], __builtin_fmaf(bb[i % QG], X[rb][i], yacc[ri][rb][i]));
+    }
+  }
+
+  // ---- 5. reduce the waves (fixed order) and store --------------------------
+  __syncthreads();  // every wave is done with its LDS region
+  f32x4_t* red = reinterpret_cast<f32x4_t*>(smem);  // [nw][R * MB][64]
+#pragma unroll
+  for (int ri = 0; ri < R; ri++)
+#pragma unroll
+    for (int rb = 0; rb < MB; rb++) red[(wave * R * MB + ri * MB + rb) * 64 + lane] = yacc[ri][rb];
+  __syncthreads();
+  if (wave < R * MB) {
+    const int ri = wave / MB, rb = wave % MB;
+    f32x4_t acc = red[wave * 64 + lane];
+    for (int wv = 1; wv < nw; wv++) {
+      const f32x4_t o = red[(wv * R * MB + wave) * 64 + lane];
+      acc[0] += o[0];
+      acc[1] += o[1];
+      acc[2] += o[2];
+      acc[3] += o[3];
+    }
+    const int n = n0 + 16 * ri + ln;
+#pragma unroll
+    for (int i = 0; i < 4; i += QG) {
+      const int m = (16 * rb + 4 * lq + i) / QG;
+      float v = 0.f;
+#pragma unroll
+      for (int q = 0; q < QG; q++) v += acc[i + q];
+      if (m < M && n < N) y[(int64_t)m * N + n] = (uint16_t)Conv<T>::to_bits(v);
     }
   }
 }
@@ -216,40 +289,86 @@ __global__ void __launch_bounds__(256) qmm_generic_kernel(const void* __restrict
   Conv<T>::store(y, m * N + n, acc);
 }
 
-template <typename T, int BITS, int GS, int MB>
-int launch_qmv_mb(const void* x, int64_t batch, int64_t M, int64_t K, const uint32_t* w, const void* scales,
-                  const void* biases, int64_t w_rep, int64_t N, void* y, hipStream_t s) {
-  // waves per workgroup: enough for ~8 waves per CU over the launch, capped
-  // so the LDS reduction (NW * MB KiB) stays small
-  const int64_t groups = (N + 15) / 16 * batch;
-  const int64_t want_waves = (int64_t)mlxq::device_cu_count() * 8;
-  int nw = 1;
-  while (nw < 8 && groups * nw < want_waves && (K / 64) / (2 * nw) >= 2) nw *= 2;
-  dim3 grid((unsigned)((N + 15) / 16), (unsigned)batch);
-#define QMV_LAUNCH(NWV)                                                                                      \
-  hipLaunchKernelGGL((qmv_mfma_kernel<T, BITS, GS, MB, NWV>), grid, dim3(NWV * 64), 0, s, (const uint16_t*)x, M, K, \
-                     w, (const uint16_t*)scales, (const uint16_t*)biases, N, w_rep, (uint16_t*)y)
-  switch (nw) {
-    case 1: QMV_LAUNCH(1); break;
-    case 2: QMV_LAUNCH(2); break;
-    case 4: QMV_LAUNCH(4); break;
-    default: QMV_LAUNCH(8); break;
+// Launch geometry for the qmv kernel, or false when the shape does not fit
+// it (then the general kernels run).
+struct QmvPlan {
+  int R, TPW, NW, MB, MR;
+  size_t lds;
+};
+
+// MLXQ_QMV_TPW (4, 8 or 16) overrides the tiles each wave streams.
+int qmv_tpw_override() {
+  static const int v = [] {
+    const char* e = getenv("MLXQ_QMV_TPW");
+    return e ? atoi(e) : 0;
+  }();
+  return v;
+}
+
+bool plan_qmv(int bits, int gs, int64_t M, int64_t K, int64_t N, int64_t batch, QmvPlan* p) {
+  const int tile_k = 512 / bits;
+  const int qg = tile_k > gs ? tile_k / gs : 1;
+  const int64_t G = K / gs;
+  // scales stage in 8-byte chunks of 4 groups
+  if (K % tile_k || K % gs || qg > 2 || G % 4) return false;
+  const int64_t rows = M * qg;
+  p->MB = rows <= 16 ? 1 : (rows <= 32 ? 2 : 0);
+  if (!p->MB) return false;
+  p->MR = (p->MB == 1 && rows <= 2) ? 2 : 4;
+  const int64_t kt = K / tile_k;
+  p->TPW = 0;
+  const int ov = qmv_tpw_override();
+  for (int tpw : {4, 8, 16}) {
+    if ((kt + tpw - 1) / tpw <= 8 && (int64_t)tpw * tile_k / gs % 4 == 0 && (ov == 0 || ov == tpw)) {
+      p->TPW = tpw;
+      break;
+    }
   }
-#undef QMV_LAUNCH
-  MLXQ_LAUNCHED("qmv_mfma_kernel");
-  return MLXQ_OK;
+  if (!p->TPW) return false;
+  p->NW = (int)((kt + p->TPW - 1) / p->TPW);
+  // two row tiles per workgroup when that still gives every CU a workgroup
+  p->R = ((N + 31) / 32) * batch >= (int64_t)mlxq::device_cu_count() ? 2 : 1;
+  const int64_t xpw = (int64_t)p->TPW * tile_k, ngw = xpw / gs;
+  const size_t wave_lds = (size_t)(M + 1) * xpw * 2 + (size_t)ngw * 16 * p->R * 8;
+  const size_t rbytes = (size_t)p->NW * p->R * p->MB * 64 * 16;
+  p->lds = (size_t)p->NW * wave_lds > rbytes ? (size_t)p->NW * wave_lds : rbytes;
+  // x slice staging: at most 8 chunks of 8 values per lane; scales: 64 chunks per lane-round
+  return p->lds <= 128 * 1024 && M * xpw <= 8 * 8 * 64;
+}
+
+template <typename T, int BITS, int GS, int MB, int R, int TPW, int MR>
+int launch_qmv_inst(const void* x, int64_t batch, int64_t M, int64_t K, const uint32_t* w, const void* scales,
+                    const void* biases, int64_t w_rep, int64_t N, void* y, const QmvPlan& p, hipStream_t s) {
+  if constexpr (TPW * (512 / BITS) / GS % 4 != 0) {
+    return mlxq::fail(MLXQ_ERR_UNSUPPORTED, "qmv: tile geometry");
+  } else {
+    auto kern = qmv_kernel<T, BITS, GS, MB, R, TPW, MR>;
+    if (p.lds > 64 * 1024) {
+      static bool raised = false;  // per instantiation
+      if (!raised) {
+        MLXQ_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024));
+        raised = true;
+      }
+    }
+    dim3 grid((unsigned)((N + 16 * R - 1) / (16 * R)), (unsigned)batch);
+    hipLaunchKernelGGL(kern, grid, dim3(p.NW * 64), p.lds, s, (const uint16_t*)x, (int)M, (int)K, w,
+                       (const uint16_t*)scales, (const uint16_t*)biases, (int)N, (int)w_rep, (uint16_t*)y);
+    MLXQ_LAUNCHED("qmv_kernel");
+    return MLXQ_OK;
+  }
 }
 
 template <typename T, int BITS, int GS>
 int launch_qmv(const void* x, int64_t batch, int64_t M, int64_t K, const uint32_t* w, const void* scales,
-               const void* biases, int64_t w_rep, int64_t N, void* y, hipStream_t s) {
-  switch ((M + 15) / 16) {
-    case 1: return launch_qmv_mb<T, BITS, GS, 1>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);
-    case 2: return launch_qmv_mb<T, BITS, GS, 2>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);
-    case 3: return launch_qmv_mb<T, BITS, GS, 3>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);
-    case 4: return launch_qmv_mb<T, BITS, GS, 4>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);
-    default: return mlxq::fail(MLXQ_ERR_UNSUPPORTED, "qmv: M > 64");
-  }
+               const void* biases, int64_t w_rep, int64_t N, void* y, const QmvPlan& p, hipStream_t s) {
+#define QMV_I(MBV, RV, TV, MRV)                                                                                 \
+  if (p.MB == MBV && p.R == RV && p.TPW == TV && p.MR == MRV)                                                   \
+    return launch_qmv_inst<T, BITS, GS, MBV, RV, TV, MRV>(x, batch, M, K, w, scales, biases, w_rep, N, y, p, s);
+  QMV_I(1, 1, 4, 2) QMV_I(1, 1, 8, 2) QMV_I(1, 1, 16, 2) QMV_I(1, 2, 4, 2) QMV_I(1, 2, 8, 2) QMV_I(1, 2, 16, 2)
+  QMV_I(1, 1, 4, 4) QMV_I(1, 1, 8, 4) QMV_I(1, 1, 16, 4) QMV_I(1, 2, 4, 4) QMV_I(1, 2, 8, 4) QMV_I(1, 2, 16, 4)
+  QMV_I(2, 1, 4, 4) QMV_I(2, 1, 8, 4) QMV_I(2, 1, 16, 4) QMV_I(2, 2, 4, 4) QMV_I(2, 2, 8, 4) QMV_I(2, 2, 16, 4)
+#undef QMV_I
+  return mlxq::fail(MLXQ_ERR_UNSUPPORTED, "qmv: no instance for this plan");
 }
 
 }  // namespace
@@ -271,23 +390,25 @@ extern "C" int mlxq_quantized_matmul(const void* x, int dtype, int64_t batch, in
   const int64_t w_rep = batch / w_batch;
   if (K == 0) return mlxq_fill_zero(y, (uint64_t)(batch * M * N * mlxq::dtype_bytes(dtype)), stream);
 
-  const bool mfma_ok = transpose && mlxq::is_half_dtype(dtype) && (bits == 4 || bits == 8) &&
-                       (group_size == 64 || group_size == 128) && K % 64 == 0 && M <= 64 &&
-                       (uintptr_t)x % 16 == 0 && (uintptr_t)w % 16 == 0;
-  if (mfma_ok) {
+  QmvPlan plan;
+  const bool qmv_ok = transpose && mlxq::is_half_dtype(dtype) && (bits == 4 || bits == 8) &&
+                      (group_size == 64 || group_size == 128) && (uintptr_t)x % 16 == 0 &&
+                      (uintptr_t)w % 16 == 0 && (uintptr_t)scales % 8 == 0 && (uintptr_t)biases % 8 == 0 &&
+                      K * M < ((int64_t)1 << 30) &&
+                      plan_qmv(bits, group_size, M, K, N, batch, &plan);
+  if (qmv_ok) {
     if (dtype == MLXQ_BFLOAT16) {
       if (bits == 4)
-        return group_size == 64 ? launch_qmv<BF16, 4, 64>(x, batch, M, K, w, scales, biases, w_rep, N, y, s)
-                                : launch_qmv<BF16, 4, 128>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);
-      return group_size == 64 ? launch_qmv<BF16, 8, 64>(x, batch, M, K, w, scales, biases, w_rep, N, y, s)
-                              : launch_qmv<BF16, 8, 128>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);
-    } else {
-      if (bits == 4)
-        return group_size == 64 ? launch_qmv<F16, 4, 64>(x, batch, M, K, w, scales, biases, w_rep, N, y, s)
-                                : launch_qmv<F16, 4, 128>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);
-      return group_size == 64 ? launch_qmv<F16, 8, 64>(x, batch, M, K, w, scales, biases, w_rep, N, y, s)
-                              : launch_qmv<F16, 8, 128>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);
+        return group_size == 64 ? launch_qmv<BF16, 4, 64>(x, batch, M, K, w, scales, biases, w_rep, N, y, plan, s)
+                                : launch_qmv<BF16, 4, 128>(x, batch, M, K, w, scales, biases, w_rep, N, y, plan, s);
+      return group_size == 64 ? launch_qmv<BF16, 8, 64>(x, batch, M, K, w, scales, biases, w_rep, N, y, plan, s)
+                              : launch_qmv<BF16, 8, 128>(x, batch, M, K, w, scales, biases, w_rep, N, y, plan, s);
     }
+    if (bits == 4)
+      return group_size == 64 ? launch_qmv<F16, 4, 64>(x, batch, M, K, w, scales, biases, w_rep, N, y, plan, s)
+                              : launch_qmv<F16, 4, 128>(x, batch, M, K, w, scales, biases, w_rep, N, y, plan, s);
+    return group_size == 64 ? launch_qmv<F16, 8, 64>(x, batch, M, K, w, scales, biases, w_rep, N, y, plan, s)
+                            : launch_qmv<F16, 8, 128>(x, batch, M, K, w, scales, biases, w_rep, N, y, plan, s);
   }
 
   const int64_t outs = M * N;

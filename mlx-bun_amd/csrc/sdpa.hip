@@ -73,18 +73,6 @@ __device__ __forceinline__ uint16_t group_bits(const uint32_t (&o)[(G + 1) / 2],
   return (uint16_t)(o[g >> 1] >> (16 * (g & 1)));
 }
 
-// Raw buffer resource over `bytes` bytes from `base` (gfx9 descriptor word 3
-// = 0x00020000): loads past the end return 0.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
-__device__ __forceinline__ uint32_t buf_load32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-  return __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0);
-}
-__device__ __forceinline__ u32x4_t buf_load128(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
-}
-
 // One cache row's G group scales (or biases): 2G contiguous bytes.
 template <int G>
 __device__ __forceinline__ void load_row_groups_buf(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
