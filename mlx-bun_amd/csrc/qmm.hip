@@ -243,6 +243,205 @@ __global__ void __launch_bounds__(512) qmv_kernel(const uint16_t* __restrict__ x
   }
 }
 
+// ---- dequantize-to-LDS MFMA GEMM (transpose = true, larger M) ------------
+//
+// The large-M path (MLX dequantizes weight tiles into threadgroup memory for
+// its qmm as well): per K-step of 64 codes the workgroup's BN weight rows are
+// dequantized (fp32 w = s * c + b) into LDS as a pair of T values, hi = T(w)
+// and lo = T(w - hi), next to the BM x 64 tile of x; 32x32x16 MFMAs read both
+// from LDS and accumulate x * hi + x * lo in fp32.  hi + lo carries w to
+// about 2^-16 relative (a single T rounding costs ~1% on a K = 14336 dot
+// product, outside the fp32-reference tolerance).
+// LDS is double-buffered: the next K-step's codes and x are loaded into
+// registers while the current one computes, then dequantized into the other
+// buffer; one barrier per K-step.  Rows past M / N read zeros (buffer loads
+// past the descriptor's end) and are not stored.
+typedef __bf16 bf16x8v __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8v __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+template <typename T>
+__device__ __forceinline__ f32x16_t mma32(u32x4_t a, u32x4_t b, f32x16_t c) {
+  if constexpr (std::is_same<T, BF16>::value)
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8v, a), __builtin_bit_cast(bf16x8v, b), c, 0,
+                                                   0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8v, a), __builtin_bit_cast(f16x8v, b), c, 0,
+                                                  0, 0);
+}
+
+// 8 codes -> 8 dequantized values w = s * c + b as T pairs: hi = T(w),
+// lo = T(w - hi)
+template <typename T, int BITS>
+__device__ __forceinline__ void dequant8(uint32_t w0, uint32_t w1, float s, float b, u32x4_t& hi, u32x4_t& lo) {
+  float v[8];
+  if constexpr (BITS == 4) {
+#pragma unroll
+    for (int e = 0; e < 8; e++) v[e] = __builtin_fmaf(s, (float)((w0 >> (4 * e)) & 0xfu), b);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      v[e] = __builtin_fmaf(s, (float)((w0 >> (8 * e)) & 0xffu), b);
+      v[4 + e] = __builtin_fmaf(s, (float)((w1 >> (8 * e)) & 0xffu), b);
+    }
+  }
+  uint32_t h[4], l[4];
+#pragma unroll
+  for (int p = 0; p < 4; p++) {
+    h[p] = Mma<T>::pack2(v[2 * p], v[2 * p + 1]);
+    const float h0 = Conv<T>::from_bits(h[p] & 0xffffu), h1 = Conv<T>::from_bits(h[p] >> 16);
+    l[p] = Mma<T>::pack2(v[2 * p] - h0, v[2 * p + 1] - h1);
+  }
+  hi = u32x4_t{h[0], h[1], h[2], h[3]};
+  lo = u32x4_t{l[0], l[1], l[2], l[3]};
+}
+
+template <typename T, int BITS, int GS, int BM, int BN>
+__global__ void __launch_bounds__(256) qmm_lds_kernel(const uint16_t* __restrict__ x, int M, int K,
+                                                      const uint32_t* __restrict__ w,
+                                                      const uint16_t* __restrict__ scales,
+                                                      const uint16_t* __restrict__ biases, int N, int w_rep,
+                                                      uint16_t* __restrict__ y) {
+  constexpr int BK = 64, PITCH = BK + 8;            // LDS row pitch in T elements (bank spread)
+  constexpr int WM = BM / 2, WN = BN / 2;            // wave tile (2 x 2 waves)
+  constexpr int TM = WM / 32, TN = WN / 32;          // 32x32 MFMA tiles per wave
+  constexpr int XL = BM * BK / 8 / 256;              // x 16-byte chunks per thread
+  constexpr int CW = BK * BITS / 32;                 // code words per weight row per K-step
+  constexpr int WCH = BN * CW / 4;                   // weight 16-byte chunks per K-step
+  constexpr int WL = (WCH + 255) / 256;              // ... per thread
+  static_assert(XL >= 1 && BM * BK / 8 % 256 == 0, "x tile must split evenly over 256 threads");
+  __shared__ __align__(16) uint16_t xs[2][BM * PITCH];
+  __shared__ __align__(16) uint16_t ws[2][2][BN * PITCH];  // [buffer][hi, lo]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN, bidx = blockIdx.z, wb = bidx / w_rep;
+  const int G = K / GS;
+  const uint32_t row_bytes = (uint32_t)K * BITS / 8;
+  const int mrows = min(BM, M - m0), nrows = min(BN, N - n0);
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + ((int64_t)bidx * M + m0) * K, (uint32_t)(mrows * K * 2));
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(w + ((int64_t)wb * N + n0) * (row_bytes / 4), (uint32_t)nrows * row_bytes);
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(scales + ((int64_t)wb * N + n0) * G, (uint32_t)(nrows * G * 2));
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(biases + ((int64_t)wb * N + n0) * G, (uint32_t)(nrows * G * 2));
+
+  // per-thread chunk coordinates: x chunk c -> row c / 8, k 8 (c % 8);
+  // weight chunk c -> row c / (CW / 4), words 4 (c % (CW / 4))
+  u32x4_t xr[XL], wr[WL];
+  uint32_t sr[WL], br[WL];
+  auto load = [&](int kt) {
+    const uint32_t k0 = (uint32_t)kt * BK;
+#pragma unroll
+    for (int i = 0; i < XL; i++) {
+      const int c = tid + 256 * i;
+      xr[i] = buf_load128(rx, ((uint32_t)(c / 8) * (uint32_t)K + k0 + 8u * (c % 8)) * 2u, 0u);
+    }
+#pragma unroll
+    for (int i = 0; i < WL; i++) {
+      const int c = tid + 256 * i, r = c / (CW / 4), q = c % (CW / 4);
+      const bool ok = WCH % 256 == 0 || c < WCH;
+      wr[i] = buf_load128(rw, ok ? (uint32_t)r * row_bytes + k0 * BITS / 8 + 16u * q : 0x80000000u, 0u);
+      const uint32_t so = ((uint32_t)r * (uint32_t)G + (k0 + 16u * q * 8u / BITS) / GS) * 2u;
+      sr[i] = buf_load16(rs, ok ? so : 0x80000000u, 0u);
+      br[i] = buf_load16(rb, ok ? so : 0x80000000u, 0u);
+    }
+  };
+  auto stash = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < XL; i++) {
+      const int c = tid + 256 * i;
+      *reinterpret_cast<u32x4_t*>(&xs[buf][(c / 8) * PITCH + 8 * (c % 8)]) = xr[i];
+    }
+#pragma unroll
+    for (int i = 0; i < WL; i++) {
+      const int c = tid + 256 * i, r = c / (CW / 4), q = c % (CW / 4);
+      if (WCH % 256 != 0 && c >= WCH) continue;
+      const float sc = Conv<T>::from_bits(sr[i]), bi = Conv<T>::from_bits(br[i]);
+      constexpr int VPW = 32 / BITS;  // values per word
+      uint16_t* dh = &ws[buf][0][r * PITCH + q * 4 * VPW];
+      uint16_t* dl = &ws[buf][1][r * PITCH + q * 4 * VPW];
+#pragma unroll
+      for (int j = 0; j < (BITS == 4 ? 4 : 2); j++) {
+        u32x4_t hv, lv;
+        if constexpr (BITS == 4)
+          dequant8<T, 4>(wr[i][j], 0u, sc, bi, hv, lv);
+        else
+          dequant8<T, 8>(wr[i][2 * j], wr[i][2 * j + 1], sc, bi, hv, lv);
+        *reinterpret_cast<u32x4_t*>(dh + 8 * j) = hv;
+        *reinterpret_cast<u32x4_t*>(dl + 8 * j) = lv;
+      }
+    }
+  };
+
+  f32x16_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
+
+  const int KT = K / BK;
+  load(0);
+  stash(0);
+  __syncthreads();
+  const int lr = lane & 31, lk = 8 * (lane >> 5);
+  for (int kt = 0; kt < KT; kt++) {
+    const int buf = kt & 1;
+    if (kt + 1 < KT) load(kt + 1);
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ks++) {
+      u32x4_t a[TM], bh[TN], bl[TN];
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+        a[i] = *reinterpret_cast<const u32x4_t*>(&xs[buf][(wm * WM + 32 * i + lr) * PITCH + 16 * ks + lk]);
+#pragma unroll
+      for (int j = 0; j < TN; j++) {
+        bh[j] = *reinterpret_cast<const u32x4_t*>(&ws[buf][0][(wn * WN + 32 * j + lr) * PITCH + 16 * ks + lk]);
+        bl[j] = *reinterpret_cast<const u32x4_t*>(&ws[buf][1][(wn * WN + 32 * j + lr) * PITCH + 16 * ks + lk]);
+      }
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = mma32<T>(a[i], bl[j], mma32<T>(a[i], bh[j], acc[i][j]));
+    }
+    if (kt + 1 < KT) stash(buf ^ 1);
+    __syncthreads();
+  }
+
+  // D[32 x 32]: lane holds column lane % 32, rows 8 (v / 4) + 4 (lane / 32) + v % 4
+  uint16_t* yb = y + (int64_t)bidx * M * N;
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+      const int n = n0 + wn * WN + 32 * j + lr;
+#pragma unroll
+      for (int v = 0; v < 16; v++) {
+        const int m = m0 + wm * WM + 32 * i + 8 * (v / 4) + 4 * (lane >> 5) + v % 4;
+        if (m < M && n < N) yb[(int64_t)m * N + n] = (uint16_t)Conv<T>::to_bits(acc[i][j][v]);
+      }
+    }
+}
+
+template <typename T, int BITS, int GS>
+int launch_qmm_lds(const void* x, int64_t batch, int64_t M, int64_t K, const uint32_t* w, const void* scales,
+                   const void* biases, int64_t w_rep, int64_t N, void* y, hipStream_t s) {
+#define QMM_L(BMV, BNV)                                                                                          \
+  {                                                                                                              \
+    dim3 grid((unsigned)((N + BNV - 1) / BNV), (unsigned)((M + BMV - 1) / BMV), (unsigned)batch);              \
+    hipLaunchKernelGGL((qmm_lds_kernel<T, BITS, GS, BMV, BNV>), grid, dim3(256), 0, s, (const uint16_t*)x, (int)M, \
+                       (int)K, w, (const uint16_t*)scales, (const uint16_t*)biases, (int)N, (int)w_rep,          \
+                       (uint16_t*)y);                                                                            \
+  }
+  // big tiles once they still give every CU a workgroup
+  if (M >= 128 && ((N + 127) / 128) * ((M + 127) / 128) * batch >= mlxq::device_cu_count())
+    QMM_L(128, 128)
+  else
+    QMM_L(64, 64)
+#undef QMM_L
+  MLXQ_LAUNCHED("qmm_lds_kernel");
+  return MLXQ_OK;
+}
+
 // ---- generic VALU path -----------------------------------------------------
 // One thread per output element; fp32 accumulation of fp32-dequantized
 // weights.  transpose=1: W [N, K] grouped along K.  transpose=0: W [K, N]
@@ -409,6 +608,27 @@ extern "C" int mlxq_quantized_matmul(const void* x, int dtype, int64_t batch, in
                               : launch_qmv<F16, 4, 128>(x, batch, M, K, w, scales, biases, w_rep, N, y, plan, s);
     return group_size == 64 ? launch_qmv<F16, 8, 64>(x, batch, M, K, w, scales, biases, w_rep, N, y, plan, s)
                             : launch_qmv<F16, 8, 128>(x, batch, M, K, w, scales, biases, w_rep, N, y, plan, s);
+  }
+
+  const bool lds_ok = transpose && mlxq::is_half_dtype(dtype) && (bits == 4 || bits == 8) && K % 64 == 0 &&
+                      (uintptr_t)x % 16 == 0 && (uintptr_t)w % 16 == 0 && (uintptr_t)scales % 2 == 0 &&
+                      M * K * 2 < ((int64_t)1 << 31) && N * K < ((int64_t)1 << 31);
+  if (lds_ok) {
+#define QMM_LDS_T(TT)                                                                                           \
+  switch (bits * 1000 + group_size) {                                                                           \
+    case 4032: return launch_qmm_lds<TT, 4, 32>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);             \
+    case 4064: return launch_qmm_lds<TT, 4, 64>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);             \
+    case 4128: return launch_qmm_lds<TT, 4, 128>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);            \
+    case 8032: return launch_qmm_lds<TT, 8, 32>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);             \
+    case 8064: return launch_qmm_lds<TT, 8, 64>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);             \
+    default: return launch_qmm_lds<TT, 8, 128>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);              \
+  }
+    if (dtype == MLXQ_BFLOAT16) {
+      QMM_LDS_T(BF16)
+    } else {
+      QMM_LDS_T(F16)
+    }
+#undef QMM_LDS_T
   }
 
   const int64_t outs = M * N;
