@@ -85,6 +85,21 @@ __device__ __forceinline__ uint32_t buf_load16(__amdgpu_buffer_rsrc_t r, uint32_
   return __builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, (int)soff, 0);
 }
 
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+// v_mfma_f32_32x32x16_{bf16,f16}: A [32 x 16] lane l = row l % 32, k slots
+// 8 (l / 32) .. + 8; B likewise by column; D [32 x 32] lane l = column
+// l % 32, rows 8 (v / 4) + 4 (l / 32) + v % 4 for v = 0..15.
+template <typename T>
+__device__ __forceinline__ f32x16_t mma32(u32x4_t a, u32x4_t b, f32x16_t c) {
+  if constexpr (std::is_same<T, BF16>::value)
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
+                                                   0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c, 0,
+                                                  0, 0);
+}
+
 __device__ __forceinline__ uint32_t perm_b32(uint32_t hi, uint32_t lo, uint32_t sel) {
   return __builtin_amdgcn_perm(hi, lo, sel);
 }

@@ -256,20 +256,6 @@ __global__ void __launch_bounds__(512) qmv_kernel(const uint16_t* __restrict__ x
 // registers while the current one computes, then dequantized into the other
 // buffer; one barrier per K-step.  Rows past M / N read zeros (buffer loads
 // past the descriptor's end) and are not stored.
-typedef __bf16 bf16x8v __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8v __attribute__((ext_vector_type(8)));
-typedef float f32x16_t __attribute__((ext_vector_type(16)));
-
-template <typename T>
-__device__ __forceinline__ f32x16_t mma32(u32x4_t a, u32x4_t b, f32x16_t c) {
-  if constexpr (std::is_same<T, BF16>::value)
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8v, a), __builtin_bit_cast(bf16x8v, b), c, 0,
-                                                   0, 0);
-  else
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8v, a), __builtin_bit_cast(f16x8v, b), c, 0,
-                                                  0, 0);
-}
-
 // 8 codes -> 8 dequantized values w = s * c + b as T pairs: hi = T(w),
 // lo = T(w - hi)
 template <typename T, int BITS>

@@ -604,6 +604,318 @@ __global__ void __launch_bounds__(256) sdpa_decode_merge_kernel(const float4* __
   Conv<T>::store(out, o + 3, Ut.w / Lt);
 }
 
+// ========================================================== MFMA prefill
+//
+// Lq > 1 (chunked prefill over the quantized cache, quantizedSdpaTiled's
+// job, src/model/gemma4-base.ts:1356-1521) is a dense contraction, so it
+// runs on the matrix cores.  A workgroup owns 256 query rows of one (batch
+// row, kv head): row r = (query i, head h) with r = i_local * nRep + h, so
+// every head of the kv head shares each K/V tile.  Per 64-key tile:
+//   * K and V codes are dequantized (fp32 s * c + b, rounded to T) into
+//     LDS: K as [key][d], V transposed as [d][key'] with the keys of every
+//     16-key group stored in the order the P operand below produces them;
+//   * each wave computes S^T = K Q^T for its 32 rows with
+//     v_mfma_f32_32x32x16 (lane l holds column (query row) l % 32 and 16
+//     keys of each 32-key block), so a row's softmax is in-lane work plus
+//     one exchange with lane l ^ 32;
+//   * online softmax in fp32 (lazy rescale), then O^T += V^T P^T where the
+//     P^T operand is exactly the lane's own probabilities packed to T.
+// Next tile's codes are loaded into registers while the current tile
+// computes; LDS is double-buffered (one barrier per tile).  Causal / window
+// masks are applied only on tiles that straddle a row's boundary.
+template <int D>
+struct PrefillShape {
+  static constexpr int BN = 64;                   // keys per tile
+  static constexpr int NW = 8;                    // waves (32 query rows each)
+  static constexpr int ROWS = 32 * NW;
+  static constexpr int KP = D + 8;                // K tile pitch (T elements)
+  static constexpr int VP = BN + 8;               // V^T tile pitch
+  static constexpr int KI = BN * D / 32;          // K items: 32 codes of one key
+  static constexpr int VI = (BN / 4) * (D / 8);   // V items: 8 codes of 4 keys
+  static constexpr int IPT = (KI + VI + NW * 64 - 1) / (NW * 64);  // items per thread
+};
+
+// position of key r (0..15) of a 16-key group in the V^T tile: the P^T
+// operand slot order (quads 1 and 2 swapped)
+__device__ __forceinline__ int vt_pos(int key) { return (key & ~15) | ((key & 4) << 1) | ((key & 8) >> 1) | (key & 3); }
+
+template <typename T, int BITS, int D, int GS>
+__global__ void __launch_bounds__(512) sdpa_prefill_mfma_kernel(
+    const uint16_t* __restrict__ q, const uint32_t* __restrict__ kp, const uint16_t* __restrict__ ksc,
+    const uint16_t* __restrict__ kbi, const uint32_t* __restrict__ vp, const uint16_t* __restrict__ vsc,
+    const uint16_t* __restrict__ vbi, int Hq, int Hkv, int Lq, Geometry geo, int causal, int window, float scale,
+    uint16_t* __restrict__ out) {
+  using SH = PrefillShape<D>;
+  constexpr int BN = SH::BN, NW = SH::NW, KP = SH::KP, VP = SH::VP, KI = SH::KI, VI = SH::VI, IPT = SH::IPT;
+  constexpr int KW = D * BITS / 32;  // code words per cache row
+  constexpr int G = D / GS;
+  constexpr int KS = D / 16;         // k-steps of S^T
+  constexpr int DB = D / 32;         // O^T row blocks
+  constexpr uint32_t CMASK = (1u << BITS) - 1u;
+  __shared__ __align__(16) uint16_t kt_lds[2][BN * KP];
+  __shared__ __align__(16) uint16_t vt_lds[2][D * VP];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lc = lane & 31, lh = lane >> 5;
+  const int b = blockIdx.z, kvh = blockIdx.y;
+  const int nrep = Hq / Hkv;
+  const int64_t valid = row_valid(geo, b);
+  const int64_t rowbase = ((int64_t)b * Hkv + kvh) * geo.cap;  // slot 0 of this (b, kvh)
+
+  // ---- this lane's query row --------------------------------------------
+  const int r = blockIdx.x * SH::ROWS + wave * 32 + lc;  // (query, head) row
+  const int qi = r / nrep, h = r % nrep;
+  const bool row_ok = qi < Lq;
+  const int64_t pos = valid - Lq + (row_ok ? qi : Lq - 1);  // logical position of the query
+  // key range of the workgroup (rows are ordered by query index)
+  const int qi_lo = blockIdx.x * SH::ROWS / nrep;
+  const int qi_hi = min(Lq - 1, (blockIdx.x * SH::ROWS + SH::ROWS - 1) / nrep);
+  int64_t kend = valid, kbeg = 0;
+  if (causal) kend = min(kend, valid - Lq + qi_hi + 1);
+  if (window > 0) kbeg = max((int64_t)0, valid - Lq + qi_lo - window + 1);
+  kbeg = kbeg / BN * BN;
+  // this wave's own row range, for the "tile needs no mask" test
+  const int wq_lo = min(Lq - 1, (blockIdx.x * SH::ROWS + wave * 32) / nrep);
+  const int64_t wpos_lo = valid - Lq + wq_lo;
+
+  // ---- q' = T(q * T(scale)) as the B operand of S^T -----------------------
+  const float scale_t = Conv<T>::round(scale);
+  const bool apply_scale = scale != 1.0f;
+  u32x4_t qop[KS];
+  {
+    const uint16_t* qrow = q + (((int64_t)b * Hq + (int64_t)kvh * nrep + h) * Lq + (row_ok ? qi : 0)) * D;
+#pragma unroll
+    for (int ks = 0; ks < KS; ks++) {
+      u32x4_t raw = row_ok ? *reinterpret_cast<const u32x4_t*>(qrow + 16 * ks + 8 * lh) : u32x4_t{0u, 0u, 0u, 0u};
+      if (apply_scale) {
+#pragma unroll
+        for (int p2 = 0; p2 < 4; p2++) {
+          const float lo = Conv<T>::round(Conv<T>::from_bits(raw[p2] & 0xffffu) * scale_t);
+          const float hi = Conv<T>::round(Conv<T>::from_bits(raw[p2] >> 16) * scale_t);
+          raw[p2] = Mma<T>::pack2(lo, hi);
+        }
+      }
+      qop[ks] = raw;
+    }
+  }
+
+  // ---- K/V tile loads: item it < KI is (key it / (D/32), 32 codes), else
+  // (4 keys, 8 codes) of V; loads are raw buffer loads bounded to the row's
+  // valid keys (keys past them read 0) ----------------------------------------
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kp + rowbase * KW, (uint32_t)(valid * KW * 4));
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vp + rowbase * KW, (uint32_t)(valid * KW * 4));
+  const __amdgpu_buffer_rsrc_t rks = make_rsrc(ksc + rowbase * G, (uint32_t)(valid * G * 2));
+  const __amdgpu_buffer_rsrc_t rkb = make_rsrc(kbi + rowbase * G, (uint32_t)(valid * G * 2));
+  const __amdgpu_buffer_rsrc_t rvs = make_rsrc(vsc + rowbase * G, (uint32_t)(valid * G * 2));
+  const __amdgpu_buffer_rsrc_t rvb = make_rsrc(vbi + rowbase * G, (uint32_t)(valid * G * 2));
+  constexpr int KIW = 32 * BITS / 32;  // words per K item (4 or 8)
+  constexpr int VIW = 8 * BITS / 32;   // words per key of a V item (1 or 2)
+  uint32_t reg_w[IPT][8];
+  uint32_t reg_s[IPT][4], reg_b[IPT][4];
+  auto load = [&](int64_t k0) {
+#pragma unroll
+    for (int u = 0; u < IPT; u++) {
+      const int it = tid + u * NW * 64;
+      if (it < KI) {
+        const int key = it / (D / 32), qd = it % (D / 32);
+        const uint32_t roff = (uint32_t)(k0 + key) * (uint32_t)(KW * 4) + (uint32_t)qd * KIW * 4;
+        const u32x4_t w0 = buf_load128(rk, roff, 0u);
+        reg_w[u][0] = w0.x; reg_w[u][1] = w0.y; reg_w[u][2] = w0.z; reg_w[u][3] = w0.w;
+        if constexpr (KIW == 8) {
+          const u32x4_t w1 = buf_load128(rk, roff + 16u, 0u);
+          reg_w[u][4] = w1.x; reg_w[u][5] = w1.y; reg_w[u][6] = w1.z; reg_w[u][7] = w1.w;
+        }
+        const uint32_t so = ((uint32_t)(k0 + key) * G + (uint32_t)(32 * qd / GS)) * 2u;
+        reg_s[u][0] = buf_load16(rks, so, 0u);
+        reg_b[u][0] = buf_load16(rkb, so, 0u);
+      } else if (it < KI + VI) {
+        const int vi = it - KI, kq = vi / (D / 8), d8 = vi % (D / 8);
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) {
+          const uint32_t roff = (uint32_t)(k0 + 4 * kq + kk) * (uint32_t)(KW * 4) + (uint32_t)d8 * VIW * 4;
+          if constexpr (VIW == 1) {
+            reg_w[u][kk] = buf_load32(rv, roff, 0u);
+          } else {
+            const auto v2 = __builtin_amdgcn_raw_buffer_load_b64(rv, (int)roff, 0, 0);
+            reg_w[u][2 * kk] = v2[0];
+            reg_w[u][2 * kk + 1] = v2[1];
+          }
+          const uint32_t so = ((uint32_t)(k0 + 4 * kq + kk) * G + (uint32_t)(8 * d8 / GS)) * 2u;
+          reg_s[u][kk] = buf_load16(rvs, so, 0u);
+          reg_b[u][kk] = buf_load16(rvb, so, 0u);
+        }
+      }
+    }
+  };
+  auto stash = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < IPT; u++) {
+      const int it = tid + u * NW * 64;
+      if (it < KI) {
+        const int key = it / (D / 32), qd = it % (D / 32);
+        const float sc = Conv<T>::from_bits(reg_s[u][0]), bi = Conv<T>::from_bits(reg_b[u][0]);
+        uint16_t* dst = &kt_lds[buf][key * KP + 32 * qd];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {  // 8 codes -> 8 T values
+          float v[8];
+#pragma unroll
+          for (int e = 0; e < 8; e++) {
+            const int ci = 8 * j + e;  // code index inside the item
+            const uint32_t wv = reg_w[u][ci * BITS / 32];
+            v[e] = __builtin_fmaf(sc, (float)((wv >> ((ci * BITS) % 32)) & CMASK), bi);
+          }
+          *reinterpret_cast<u32x4_t*>(dst + 8 * j) = u32x4_t{Mma<T>::pack2(v[0], v[1]), Mma<T>::pack2(v[2], v[3]),
+                                                             Mma<T>::pack2(v[4], v[5]), Mma<T>::pack2(v[6], v[7])};
+        }
+      } else if (it < KI + VI) {
+        const int vi = it - KI, kq = vi / (D / 8), d8 = vi % (D / 8);
+        float sc[4], bi[4];
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) {
+          sc[kk] = Conv<T>::from_bits(reg_s[u][kk]);
+          bi[kk] = Conv<T>::from_bits(reg_b[u][kk]);
+        }
+        const int p0 = vt_pos(4 * kq);  // the 4 keys stay adjacent
+#pragma unroll
+        for (int e = 0; e < 8; e++) {  // d = 8 d8 + e
+          float v[4];
+#pragma unroll
+          for (int kk = 0; kk < 4; kk++) {
+            const uint32_t wv = reg_w[u][kk * VIW + e * BITS / 32];
+            v[kk] = __builtin_fmaf(sc[kk], (float)((wv >> ((e * BITS) % 32)) & CMASK), bi[kk]);
+          }
+          *reinterpret_cast<uint2*>(&vt_lds[buf][(8 * d8 + e) * VP + p0]) =
+              make_uint2(Mma<T>::pack2(v[0], v[1]), Mma<T>::pack2(v[2], v[3]));
+        }
+      }
+    }
+  };
+
+  f32x16_t oacc[DB];
+#pragma unroll
+  for (int i = 0; i < DB; i++)
+#pragma unroll
+    for (int e = 0; e < 16; e++) oacc[i][e] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+
+  if (kbeg < kend) {
+    load(kbeg);
+    stash(0);
+  }
+  __syncthreads();
+  int buf = 0;
+  for (int64_t k0 = kbeg; k0 < kend; k0 += BN) {
+    const bool more = k0 + BN < kend;
+    if (more) load(k0 + BN);
+    // ---- S^T: two 32-key blocks --------------------------------------------
+    f32x16_t sacc[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) sacc[kb][e] = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < KS; ks++) {
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++) {
+        const u32x4_t a = *reinterpret_cast<const u32x4_t*>(&kt_lds[buf][(32 * kb + lc) * KP + 16 * ks + 8 * lh]);
+        sacc[kb] = mma32<T>(a, qop[ks], sacc[kb]);
+      }
+    }
+    // ---- online softmax over this lane's 32 keys (+ lane ^ 32's) -----------
+    // key of sacc[kb][v]: k0 + 32 kb + 8 (v / 4) + 4 lh + v % 4
+    const bool need_mask = k0 + BN > valid || (causal && k0 + BN - 1 > wpos_lo) ||
+                           (window > 0 && k0 <= valid - Lq + min(Lq - 1, wq_lo + 32) - window);
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+      for (int v = 0; v < 16; v++) {
+        float sv = sacc[kb][v] * LOG2E;
+        if (need_mask) {  // wave-uniform
+          const int64_t j = k0 + 32 * kb + 8 * (v / 4) + 4 * lh + v % 4;
+          const bool ok = j < valid && (!causal || j <= pos) && (window <= 0 || pos < j + window) && row_ok;
+          sv = ok ? sv : -INFINITY;
+        }
+        sacc[kb][v] = sv;
+        tmax = fmaxf(tmax, sv);
+      }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    const float m_old = m_run;
+    const float m_new = tmax > m_old + 8.0f ? tmax : m_old;  // lazy: p <= 2^8
+    const float alpha = m_new == m_old ? 1.0f : __builtin_amdgcn_exp2f(m_old - m_new);
+    const float m_sub = m_new == -INFINITY ? 0.0f : m_new;
+    m_run = m_new;
+    float psum = 0.f;
+    uint32_t pk[2][8];  // P as T pairs: [block][pair]
+#pragma unroll
+    for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+      for (int v = 0; v < 16; v += 2) {
+        const float p0 = __builtin_amdgcn_exp2f(sacc[kb][v] - m_sub);
+        const float p1 = __builtin_amdgcn_exp2f(sacc[kb][v + 1] - m_sub);
+        psum += p0 + p1;
+        pk[kb][v / 2] = Mma<T>::pack2(p0, p1);
+      }
+    l_run = l_run * alpha + psum;
+    if (__any(alpha != 1.0f)) {
+#pragma unroll
+      for (int i = 0; i < DB; i++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) oacc[i][e] *= alpha;
+    }
+    // ---- O^T += V^T P^T: four 16-key k-steps --------------------------------
+#pragma unroll
+    for (int m = 0; m < 4; m++) {
+      const int kb = m / 2, vo = 4 * (m % 2);
+      const u32x4_t bop = {pk[kb][vo], pk[kb][vo + 1], pk[kb][vo + 2], pk[kb][vo + 3]};
+#pragma unroll
+      for (int i = 0; i < DB; i++) {
+        const u32x4_t a = *reinterpret_cast<const u32x4_t*>(&vt_lds[buf][(32 * i + lc) * VP + 16 * m + 8 * lh]);
+        oacc[i] = mma32<T>(a, bop, oacc[i]);
+      }
+    }
+    if (more) stash(buf ^ 1);
+    __syncthreads();
+    buf ^= 1;
+  }
+
+  // ---- normalise and store: lane holds d = 32 i + 8 (v / 4) + 4 lh + v % 4 --
+  const float lt = l_run + __shfl_xor(l_run, 32);
+  const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+  if (row_ok) {
+    uint16_t* orow = out + (((int64_t)b * Hq + (int64_t)kvh * nrep + h) * Lq + qi) * D;
+#pragma unroll
+    for (int i = 0; i < DB; i++)
+#pragma unroll
+      for (int v = 0; v < 16; v += 4) {
+        const int d = 32 * i + 8 * (v / 4) + 4 * lh;
+        *reinterpret_cast<uint2*>(orow + d) = make_uint2(Mma<T>::pack2(oacc[i][v] * inv, oacc[i][v + 1] * inv),
+                                                         Mma<T>::pack2(oacc[i][v + 2] * inv, oacc[i][v + 3] * inv));
+      }
+  }
+}
+
+template <typename T, int BITS>
+int launch_prefill(int D, int gs, const void* q, int B, int Hq, int Hkv, int Lq, const uint32_t* kp, const void* ks,
+                   const void* kb, const uint32_t* vp, const void* vs, const void* vb, Geometry geo, int causal,
+                   int window, float scale, void* out, hipStream_t s) {
+  const int nrep = Hq / Hkv;
+  const int64_t rows = (int64_t)Lq * nrep;
+#define PRE(DV, GV)                                                                                            \
+  if (D == DV && gs == GV) {                                                                                   \
+    dim3 grid((unsigned)((rows + PrefillShape<DV>::ROWS - 1) / PrefillShape<DV>::ROWS), (unsigned)Hkv, (unsigned)B); \
+    hipLaunchKernelGGL((sdpa_prefill_mfma_kernel<T, BITS, DV, GV>), grid, dim3(512), 0, s, (const uint16_t*)q, kp, \
+                       (const uint16_t*)ks, (const uint16_t*)kb, vp, (const uint16_t*)vs, (const uint16_t*)vb, Hq, Hkv, \
+                       Lq, geo, causal, window, scale, (uint16_t*)out);                                        \
+    MLXQ_LAUNCHED("sdpa_prefill_mfma_kernel");                                                                 \
+    return MLXQ_OK;                                                                                            \
+  }
+  PRE(64, 32) PRE(64, 64) PRE(128, 32) PRE(128, 64) PRE(128, 128)
+#undef PRE
+  return mlxq::fail(MLXQ_ERR_UNSUPPORTED, "prefill: no MFMA instance for this head_dim/group_size");
+}
+
 // ========================================================== generic kernel
 // One workgroup (128 threads) per (batch row, q head, query).  Scores for
 // 128 keys at a time (one key per thread, fp32 dot of fp32-dequantized K),
@@ -836,6 +1148,21 @@ extern "C" int mlxq_quantized_sdpa(const void* q, int dtype, int B, int Hq, int 
                                                v_scales, v_biases, geo, scale, out, s);
   }
   const int causal = mask_mode == MLXQ_MASK_CAUSAL;
+  // Lq > 1 on the matrix cores: plain (non-ring) caches, T = bf16/f16, 4/8-bit
+  const bool prefill_ok = Lq > 1 && !ring_offset && mlxq::is_half_dtype(dtype) && (bits == 4 || bits == 8) &&
+                          (D == 64 || D == 128) && (uintptr_t)k_scales % 2 == 0 &&
+                          kv_capacity * (int64_t)D * bits / 8 < ((int64_t)1 << 31);
+  if (prefill_ok) {
+    if (dtype == MLXQ_BFLOAT16)
+      return bits == 4 ? launch_prefill<BF16, 4>(D, group_size, q, B, Hq, Hkv, Lq, k_packed, k_scales, k_biases,
+                                                 v_packed, v_scales, v_biases, geo, causal, window, scale, out, s)
+                       : launch_prefill<BF16, 8>(D, group_size, q, B, Hq, Hkv, Lq, k_packed, k_scales, k_biases,
+                                                 v_packed, v_scales, v_biases, geo, causal, window, scale, out, s);
+    return bits == 4 ? launch_prefill<F16, 4>(D, group_size, q, B, Hq, Hkv, Lq, k_packed, k_scales, k_biases, v_packed,
+                                              v_scales, v_biases, geo, causal, window, scale, out, s)
+                     : launch_prefill<F16, 8>(D, group_size, q, B, Hq, Hkv, Lq, k_packed, k_scales, k_biases, v_packed,
+                                              v_scales, v_biases, geo, causal, window, scale, out, s);
+  }
   dim3 grid((unsigned)Lq, (unsigned)Hq, (unsigned)B);
   MLXQ_DISPATCH_T(dtype, TT, {
     switch (bits) {
