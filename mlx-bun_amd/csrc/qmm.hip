@@ -34,7 +34,7 @@ namespace {
 #define QMV_WIN 2
 #endif
 
-template <typename T, int BITS, int GS, int MB, int R, int TPW, int MR>
+template <typename T, int BITS, int GS, int MB, int R, int TPW, int MR, int XC>
 __global__ void __launch_bounds__(512) qmv_kernel(const uint16_t* __restrict__ x, int M, int K,
                                                   const uint32_t* __restrict__ w,
                                                   const uint16_t* __restrict__ scales,
@@ -48,7 +48,6 @@ __global__ void __launch_bounds__(512) qmv_kernel(const uint16_t* __restrict__ x
   constexpr int SCH = 16 * R * NGW / 4;              // 8-byte scale chunks per wave
   constexpr int SPL = (SCH + 63) / 64;               // ... per lane
   constexpr int XPW = TPW * TILE_K;                  // x values per row per wave
-  constexpr int XC = 8;                              // x chunks (8 values) per lane, at most
   constexpr float OFF = CO::OFFSET;
   static_assert(QG <= 2 && NGW % 4 == 0, "tile / group geometry");
   extern __shared__ __align__(16) uint8_t smem[];
@@ -68,15 +67,17 @@ __global__ void __launch_bounds__(512) qmv_kernel(const uint16_t* __restrict__ x
   const __amdgpu_buffer_rsrc_t rb = make_rsrc(biases + ((int64_t)wb * N + n0) * G, (uint32_t)(rows * G * 2));
   // This wave's tiles [t_first, t_first + TPW) (the last wave's tail tiles
   // are clamped duplicates that add nothing) and its private LDS region:
-  // x slice [M + 1][XPW] in code-slot order (row M all zero: the A operand
-  // of lanes whose group or row is inactive), then (s, b - off s) as float2
-  // [NGW][16R].
+  // x slice [M][XPW] in code-slot order, then (s, b - off s) as float2
+  // [NGW][16R].  After all waves' regions: one zero x row [XPW] shared by the
+  // workgroup, the A operand of lanes whose group or row is inactive (every
+  // wave writes it before reading it, all with zeros).
   const int t_first = wave * TPW;
   const int k_first = t_first * TILE_K, g_first = k_first / GS;
   const int xchunks = M * XPW / 8;
-  const size_t wave_lds = (size_t)(M + 1) * XPW * 2 + (size_t)NGW * 16 * R * 8;
+  const size_t wave_lds = (size_t)M * XPW * 2 + (size_t)NGW * 16 * R * 8;
   uint16_t* xl = reinterpret_cast<uint16_t*>(smem + wave * wave_lds);
-  float2* sbl = reinterpret_cast<float2*>(smem + wave * wave_lds + (size_t)(M + 1) * XPW * 2);
+  float2* sbl = reinterpret_cast<float2*>(smem + wave * wave_lds + (size_t)M * XPW * 2);
+  uint16_t* xz = reinterpret_cast<uint16_t*>(smem + nw * wave_lds);
 
   // ---- 1. x slice and scales/biases of this wave (coalesced), issued before
   // the weight stream: vector loads complete in order, so waiting for these
@@ -128,7 +129,7 @@ __global__ void __launch_bounds__(512) qmv_kernel(const uint16_t* __restrict__ x
       if (ci < xchunks) *reinterpret_cast<u32x4_t*>(xl + ci * 8) = permute8<CO::ORDER>(xst[c]);
     }
   }
-  for (int c = lane; c < XPW / 8; c += 64) *reinterpret_cast<u32x4_t*>(xl + M * XPW + 8 * c) = u32x4_t{0u, 0u, 0u, 0u};
+  for (int c = lane; c < XPW / 8; c += 64) *reinterpret_cast<u32x4_t*>(xz + 8 * c) = u32x4_t{0u, 0u, 0u, 0u};
 #pragma unroll
   for (int c = 0; c < SPL; c++) {
     const int ci = lane + 64 * c;
@@ -151,7 +152,7 @@ __global__ void __launch_bounds__(512) qmv_kernel(const uint16_t* __restrict__ x
 #pragma unroll
   for (int rb = 0; rb < MB; rb++) {
     const int r = ln + 16 * rb, m = r / QG, qg = r % QG;
-    xa[rb] = xl + ((lq * QG / 4 == qg && m < M) ? m : M) * XPW + lq * (TILE_K / 4);
+    xa[rb] = ((lq * QG / 4 == qg && m < M) ? xl + m * XPW : xz) + lq * (TILE_K / 4);
   }
   const u32x4_t ones = {Mma<T>::ONES, Mma<T>::ONES, Mma<T>::ONES, Mma<T>::ONES};
   const uint32_t magic = opaque(Mma<T>::MAGIC);
@@ -477,7 +478,7 @@ __global__ void __launch_bounds__(256) qmm_generic_kernel(const void* __restrict
 // Launch geometry for the qmv kernel, or false when the shape does not fit
 // it (then the general kernels run).
 struct QmvPlan {
-  int R, TPW, NW, MB, MR;
+  int R, TPW, NW, MB, MR, XC;  // XC: x chunks (8 values) each lane stages, 8 or 16
   size_t lds;
 };
 
@@ -514,24 +515,26 @@ bool plan_qmv(int bits, int gs, int64_t M, int64_t K, int64_t N, int64_t batch, 
   // two row tiles per workgroup when that still gives every CU a workgroup
   p->R = ((N + 31) / 32) * batch >= (int64_t)mlxq::device_cu_count() ? 2 : 1;
   const int64_t xpw = (int64_t)p->TPW * tile_k, ngw = xpw / gs;
-  const size_t wave_lds = (size_t)(M + 1) * xpw * 2 + (size_t)ngw * 16 * p->R * 8;
+  const size_t wave_lds = (size_t)M * xpw * 2 + (size_t)ngw * 16 * p->R * 8;
   const size_t rbytes = (size_t)p->NW * p->R * p->MB * 64 * 16;
-  p->lds = (size_t)p->NW * wave_lds > rbytes ? (size_t)p->NW * wave_lds : rbytes;
-  // x slice staging: at most 8 chunks of 8 values per lane; scales: 64 chunks per lane-round
-  return p->lds <= 128 * 1024 && M * xpw <= 8 * 8 * 64;
+  const size_t sbytes = (size_t)p->NW * wave_lds + (size_t)xpw * 2;
+  p->lds = sbytes > rbytes ? sbytes : rbytes;
+  // x slice staging: 8 or 16 chunks of 8 values per lane
+  p->XC = M * xpw <= 8 * 8 * 64 ? 8 : 16;
+  return p->lds <= 160 * 1024 && M * xpw <= 16 * 8 * 64;
 }
 
-template <typename T, int BITS, int GS, int MB, int R, int TPW, int MR>
+template <typename T, int BITS, int GS, int MB, int R, int TPW, int MR, int XC>
 int launch_qmv_inst(const void* x, int64_t batch, int64_t M, int64_t K, const uint32_t* w, const void* scales,
                     const void* biases, int64_t w_rep, int64_t N, void* y, const QmvPlan& p, hipStream_t s) {
   if constexpr (TPW * (512 / BITS) / GS % 4 != 0) {
     return mlxq::fail(MLXQ_ERR_UNSUPPORTED, "qmv: tile geometry");
   } else {
-    auto kern = qmv_kernel<T, BITS, GS, MB, R, TPW, MR>;
+    auto kern = qmv_kernel<T, BITS, GS, MB, R, TPW, MR, XC>;
     if (p.lds > 64 * 1024) {
       static bool raised = false;  // per instantiation
       if (!raised) {
-        MLXQ_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024));
+        MLXQ_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
         raised = true;
       }
     }
@@ -546,12 +549,16 @@ int launch_qmv_inst(const void* x, int64_t batch, int64_t M, int64_t K, const ui
 template <typename T, int BITS, int GS>
 int launch_qmv(const void* x, int64_t batch, int64_t M, int64_t K, const uint32_t* w, const void* scales,
                const void* biases, int64_t w_rep, int64_t N, void* y, const QmvPlan& p, hipStream_t s) {
-#define QMV_I(MBV, RV, TV, MRV)                                                                                 \
-  if (p.MB == MBV && p.R == RV && p.TPW == TV && p.MR == MRV)                                                   \
-    return launch_qmv_inst<T, BITS, GS, MBV, RV, TV, MRV>(x, batch, M, K, w, scales, biases, w_rep, N, y, p, s);
-  QMV_I(1, 1, 4, 2) QMV_I(1, 1, 8, 2) QMV_I(1, 1, 16, 2) QMV_I(1, 2, 4, 2) QMV_I(1, 2, 8, 2) QMV_I(1, 2, 16, 2)
-  QMV_I(1, 1, 4, 4) QMV_I(1, 1, 8, 4) QMV_I(1, 1, 16, 4) QMV_I(1, 2, 4, 4) QMV_I(1, 2, 8, 4) QMV_I(1, 2, 16, 4)
-  QMV_I(2, 1, 4, 4) QMV_I(2, 1, 8, 4) QMV_I(2, 1, 16, 4) QMV_I(2, 2, 4, 4) QMV_I(2, 2, 8, 4) QMV_I(2, 2, 16, 4)
+#define QMV_I(MBV, RV, TV, MRV, XCV)                                                                            \
+  if (p.MB == MBV && p.R == RV && p.TPW == TV && p.MR == MRV && p.XC == XCV)                                    \
+    return launch_qmv_inst<T, BITS, GS, MBV, RV, TV, MRV, XCV>(x, batch, M, K, w, scales, biases, w_rep, N, y, p, s);
+  QMV_I(1, 1, 4, 2, 8) QMV_I(1, 1, 8, 2, 8) QMV_I(1, 1, 16, 2, 8) QMV_I(1, 2, 4, 2, 8) QMV_I(1, 2, 8, 2, 8)
+  QMV_I(1, 2, 16, 2, 8) QMV_I(1, 1, 4, 4, 8) QMV_I(1, 1, 8, 4, 8) QMV_I(1, 1, 16, 4, 8) QMV_I(1, 2, 4, 4, 8)
+  QMV_I(1, 2, 8, 4, 8) QMV_I(1, 2, 16, 4, 8) QMV_I(2, 1, 4, 4, 8) QMV_I(2, 1, 8, 4, 8) QMV_I(2, 1, 16, 4, 8)
+  QMV_I(2, 2, 4, 4, 8) QMV_I(2, 2, 8, 4, 8) QMV_I(2, 2, 16, 4, 8)
+  // larger x slices (e.g. M = 4 at K = 14336, M = 16 at K = 4096)
+  QMV_I(1, 1, 16, 4, 16) QMV_I(1, 2, 16, 4, 16) QMV_I(1, 1, 8, 4, 16) QMV_I(1, 2, 8, 4, 16)
+  QMV_I(2, 1, 4, 4, 16) QMV_I(2, 2, 4, 4, 16) QMV_I(2, 1, 8, 4, 16) QMV_I(2, 2, 8, 4, 16)
 #undef QMV_I
   return mlxq::fail(MLXQ_ERR_UNSUPPORTED, "qmv: no instance for this plan");
 }
