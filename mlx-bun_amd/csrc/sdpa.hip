@@ -283,12 +283,26 @@ __global__ void __launch_bounds__(512) sdpa_decode_mfma_kernel(
         kb[sub][w4 + 3] = v.w;
       }
     }
+    // lane ln takes words VM ln .. VM ln + VM - 1 of each of its 8 keys:
+    // one load per key, and 16 lanes cover whole cache rows
 #pragma unroll
     for (int e = 0; e < 8; e++) {
       const uint32_t koff = (uint32_t)(e < 4 ? 4 * lg + e : 16 + 4 * lg + (e - 4));
-      const uint32_t voff = (koff * KW + ln) * 4u;
-#pragma unroll
-      for (int m = 0; m < VM; m++) vb[e][m] = buf_load32(rv, voff + 64u * m, kt * (uint32_t)(KW * 4));
+      const uint32_t voff = (koff * KW + VM * ln) * 4u;
+      const uint32_t soff = kt * (uint32_t)(KW * 4);
+      if constexpr (VM == 1) {
+        vb[e][0] = buf_load32(rv, voff, soff);
+      } else if constexpr (VM == 2) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(rv, (int)voff, (int)soff, 0);
+        vb[e][0] = v[0];
+        vb[e][1] = v[1];
+      } else {
+        const u32x4_t v = buf_load128(rv, voff, soff);
+        vb[e][0] = v.x;
+        vb[e][1] = v.y;
+        vb[e][2] = v.z;
+        vb[e][3] = v.w;
+      }
     }
   };
 #pragma unroll
@@ -436,7 +450,7 @@ __global__ void __launch_bounds__(512) sdpa_decode_mfma_kernel(
     }
     if constexpr (OFF != 0.0f) spacc = Mma<T>::mma(aop, ones, spacc);
 
-    // value MFMAs: tile (m, e') covers d = (16m + ln) * E + e'
+    // value MFMAs: tile (m, e') covers d = (VM ln + m) * E + e'
 #pragma unroll
     for (int m = 0; m < VM; m++) {
       if constexpr (BITS == 4) {
@@ -500,7 +514,7 @@ __global__ void __launch_bounds__(512) sdpa_decode_mfma_kernel(
 #pragma unroll
       for (int tt = 0; tt < DT; tt++) {
         const int m = tt / E, ep = tt % E;
-        const int d = (16 * m + ln) * E + ep;
+        const int d = (VM * ln + m) * E + ep;
         if (d / GS == g) u_lds[wave][h * D + d] = oacc[tt][i] + corr;
       }
     }
