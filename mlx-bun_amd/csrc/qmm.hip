@@ -244,117 +244,142 @@ __global__ void __launch_bounds__(512) qmv_kernel(const uint16_t* __restrict__ x
   }
 }
 
-// ---- dequantize-to-LDS MFMA GEMM (transpose = true, larger M) ------------
+// ---- tiled MFMA GEMM over exact code operands (transpose = true) ---------
 //
-// The large-M path (MLX dequantizes weight tiles into threadgroup memory for
-// its qmm as well): per K-step of 64 codes the workgroup's BN weight rows are
-// dequantized (fp32 w = s * c + b) into LDS as a pair of T values, hi = T(w)
-// and lo = T(w - hi), next to the BM x 64 tile of x; 32x32x16 MFMAs read both
-// from LDS and accumulate x * hi + x * lo in fp32.  hi + lo carries w to
-// about 2^-16 relative (a single T rounding costs ~1% on a K = 14336 dot
-// product, outside the fp32-reference tolerance).
-// LDS is double-buffered: the next K-step's codes and x are loaded into
-// registers while the current one computes, then dequantized into the other
-// buffer; one barrier per K-step.  Rows past M / N read zeros (buffer loads
-// past the descriptor's end) and are not stored.
-// 8 codes -> 8 dequantized values w = s * c + b as T pairs: hi = T(w),
-// lo = T(w - hi)
-template <typename T, int BITS>
-__device__ __forceinline__ void dequant8(uint32_t w0, uint32_t w1, float s, float b, u32x4_t& hi, u32x4_t& lo) {
-  float v[8];
-  if constexpr (BITS == 4) {
-#pragma unroll
-    for (int e = 0; e < 8; e++) v[e] = __builtin_fmaf(s, (float)((w0 >> (4 * e)) & 0xfu), b);
-  } else {
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-      v[e] = __builtin_fmaf(s, (float)((w0 >> (8 * e)) & 0xffu), b);
-      v[4 + e] = __builtin_fmaf(s, (float)((w1 >> (8 * e)) & 0xffu), b);
-    }
-  }
-  uint32_t h[4], l[4];
-#pragma unroll
-  for (int p = 0; p < 4; p++) {
-    h[p] = Mma<T>::pack2(v[2 * p], v[2 * p + 1]);
-    const float h0 = Conv<T>::from_bits(h[p] & 0xffffu), h1 = Conv<T>::from_bits(h[p] >> 16);
-    l[p] = Mma<T>::pack2(v[2 * p] - h0, v[2 * p + 1] - h1);
-  }
-  hi = u32x4_t{h[0], h[1], h[2], h[3]};
-  lo = u32x4_t{l[0], l[1], l[2], l[3]};
-}
+// The larger-M path (MLX's qmm stages weight tiles in threadgroup memory as
+// well).  A workgroup owns a BM x BN tile of y and a range of K.  Per K-step
+// of 64 codes it stages in LDS:
+//   * the x tile as T, each 8-value run permuted into the code slot order;
+//   * the weight codes as exact MFMA operands OFF + c (CodeOps);
+//   * per part of a quant group inside the step (64 values, or 32 for
+//     group_size 32): every weight row's (s, b - OFF s) and every x row's
+//     sum X of the run.
+// The 32x32x16 MFMAs contract one group part at a time into D, and the part
+// folds into the fp32 accumulators as acc += s D + (b - OFF s) X: the products
+// are exact and only fp32 accumulation rounds, so no rounding of dequantized
+// weights to T enters the result.
+// Register prefetch runs PF K-steps ahead of the LDS double buffer (one
+// barrier per step).  Workgroups of a split K (blockIdx.z = batch * KS +
+// split) write fp32 partials that qmm_splitk_reduce_kernel sums in fixed
+// split order.  Rows past M / N read zeros and are not stored.
+template <int BM, int BN>
+struct TileShape {
+  static constexpr int WGM = BM >= 64 ? 2 : 1;  // wave grid (4 waves)
+  static constexpr int WGN = 4 / WGM;
+  static constexpr int WM = BM / WGM, WN = BN / WGN;
+  static constexpr int TM = WM / 32, TN = WN / 32;  // 32x32 MFMA tiles per wave
+  static constexpr int PF = BM * BN >= 128 * 128 ? 2 : 4;
+  static_assert(TM >= 1 && TN >= 1 && WM % 32 == 0 && WN % 32 == 0, "tile shape");
+};
 
 template <typename T, int BITS, int GS, int BM, int BN>
-__global__ void __launch_bounds__(256) qmm_lds_kernel(const uint16_t* __restrict__ x, int M, int K,
-                                                      const uint32_t* __restrict__ w,
-                                                      const uint16_t* __restrict__ scales,
-                                                      const uint16_t* __restrict__ biases, int N, int w_rep,
-                                                      uint16_t* __restrict__ y) {
-  constexpr int BK = 64, PITCH = BK + 8;            // LDS row pitch in T elements (bank spread)
-  constexpr int WM = BM / 2, WN = BN / 2;            // wave tile (2 x 2 waves)
-  constexpr int TM = WM / 32, TN = WN / 32;          // 32x32 MFMA tiles per wave
-  constexpr int XL = BM * BK / 8 / 256;              // x 16-byte chunks per thread
-  constexpr int CW = BK * BITS / 32;                 // code words per weight row per K-step
-  constexpr int WCH = BN * CW / 4;                   // weight 16-byte chunks per K-step
-  constexpr int WL = (WCH + 255) / 256;              // ... per thread
-  static_assert(XL >= 1 && BM * BK / 8 % 256 == 0, "x tile must split evenly over 256 threads");
+__global__ void __launch_bounds__(256) qmm_tile_kernel(const uint16_t* __restrict__ x, int M, int K,
+                                                       const uint32_t* __restrict__ w,
+                                                       const uint16_t* __restrict__ scales,
+                                                       const uint16_t* __restrict__ biases, int N, int w_rep,
+                                                       int KS, int KTS, uint16_t* __restrict__ y,
+                                                       float* __restrict__ part) {
+  using SH = TileShape<BM, BN>;
+  using CO = CodeOps<T, BITS>;
+  constexpr int WM = SH::WM, WN = SH::WN, TM = SH::TM, TN = SH::TN, PF = SH::PF;
+  constexpr int BK = 64, PITCH = BK + 8;            // LDS row pitch in 16-bit elements (bank spread)
+  constexpr int EG = GS < BK ? GS : BK;             // K values per group part
+  constexpr int NGK = BK / EG;                      // group parts per K-step
+  constexpr int SPG = EG / 16;                      // MFMA k-steps per group part
+  constexpr int XL = BM / 32;                       // x 16-byte chunks per thread per K-step
+  constexpr int CWR = BK * BITS / 32;               // code words per weight row per K-step
+  constexpr int WPT = BN * BITS / 128;              // code words per thread per K-step
+  constexpr int UW = BITS / 4;                      // code words per 8-code unit
+  constexpr int UPT = WPT / UW;                     // 8-code units per thread
+  constexpr float OFF = CO::OFFSET;
+  static_assert(CWR % WPT == 0, "a thread's code words stay in one row");
+  static_assert(BN * NGK <= 256, "one (s, b) item per thread");
+
   __shared__ __align__(16) uint16_t xs[2][BM * PITCH];
-  __shared__ __align__(16) uint16_t ws[2][2][BN * PITCH];  // [buffer][hi, lo]
+  __shared__ __align__(16) uint16_t wc[2][BN * PITCH];
+  __shared__ __align__(16) float2 sbl[2][NGK][BN];
+  __shared__ __align__(16) float xsum[2][NGK][BM];
+
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN, bidx = blockIdx.z, wb = bidx / w_rep;
-  const int G = K / GS;
+  const int wm = wave / SH::WGN, wn = wave % SH::WGN;
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  const int bidx = blockIdx.z / KS, split = blockIdx.z % KS, wb = bidx / w_rep;
+  const int G = K / GS, KT = K / BK;
+  const int kb = split * KTS, ke = min(KT, kb + KTS);
   const uint32_t row_bytes = (uint32_t)K * BITS / 8;
   const int mrows = min(BM, M - m0), nrows = min(BN, N - n0);
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + ((int64_t)bidx * M + m0) * K, (uint32_t)(mrows * K * 2));
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(w + ((int64_t)wb * N + n0) * (row_bytes / 4), (uint32_t)nrows * row_bytes);
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(scales + ((int64_t)wb * N + n0) * G, (uint32_t)(nrows * G * 2));
   const __amdgpu_buffer_rsrc_t rb = make_rsrc(biases + ((int64_t)wb * N + n0) * G, (uint32_t)(nrows * G * 2));
+  constexpr uint32_t OOB = 0x80000000u;  // past every descriptor: reads 0
 
-  // per-thread chunk coordinates: x chunk c -> row c / 8, k 8 (c % 8);
-  // weight chunk c -> row c / (CW / 4), words 4 (c % (CW / 4))
-  u32x4_t xr[XL], wr[WL];
-  uint32_t sr[WL], br[WL];
-  auto load = [&](int kt) {
+  // thread -> staging items.  x: chunk c = tid + 256 i -> row c / 8, unit
+  // c % 8 (8 values); the 8 units of a row sit in 8 adjacent lanes.
+  // codes: words [q, q + WPT) of row wr_row.  (s, b): row sb_row, part sb_e.
+  const int wr_row = tid * WPT / CWR, wr_q = tid * WPT % CWR;
+  const int sb_row = tid / NGK, sb_e = tid % NGK;
+  const bool sb_act = tid < BN * NGK;
+
+  u32x4_t xr[PF][XL];
+  uint32_t wr[PF][WPT];
+  uint32_t sr[PF], br[PF];
+  auto load = [&](int kt, u32x4_t (&xv)[XL], uint32_t (&wv)[WPT], uint32_t& sv, uint32_t& bv) {
+    const bool ok = kt < ke;
     const uint32_t k0 = (uint32_t)kt * BK;
 #pragma unroll
     for (int i = 0; i < XL; i++) {
       const int c = tid + 256 * i;
-      xr[i] = buf_load128(rx, ((uint32_t)(c / 8) * (uint32_t)K + k0 + 8u * (c % 8)) * 2u, 0u);
+      xv[i] = buf_load128(rx, ok ? ((uint32_t)(c / 8) * (uint32_t)K + k0 + 8u * (c % 8)) * 2u : OOB, 0u);
     }
+    const uint32_t wo = ok ? (uint32_t)wr_row * row_bytes + k0 * BITS / 8 + 4u * wr_q : OOB;
+    if constexpr (WPT == 2) {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b64(rw, (int)wo, 0, 0);
+      wv[0] = v[0];
+      wv[1] = v[1];
+    } else {
 #pragma unroll
-    for (int i = 0; i < WL; i++) {
-      const int c = tid + 256 * i, r = c / (CW / 4), q = c % (CW / 4);
-      const bool ok = WCH % 256 == 0 || c < WCH;
-      wr[i] = buf_load128(rw, ok ? (uint32_t)r * row_bytes + k0 * BITS / 8 + 16u * q : 0x80000000u, 0u);
-      const uint32_t so = ((uint32_t)r * (uint32_t)G + (k0 + 16u * q * 8u / BITS) / GS) * 2u;
-      sr[i] = buf_load16(rs, ok ? so : 0x80000000u, 0u);
-      br[i] = buf_load16(rb, ok ? so : 0x80000000u, 0u);
+      for (int h = 0; h < WPT / 4; h++) {
+        const u32x4_t v = buf_load128(rw, wo + 16u * h, 0u);
+        wv[4 * h] = v.x;
+        wv[4 * h + 1] = v.y;
+        wv[4 * h + 2] = v.z;
+        wv[4 * h + 3] = v.w;
+      }
     }
+    const uint32_t so = (ok && sb_act) ? ((uint32_t)sb_row * (uint32_t)G + (k0 + (uint32_t)sb_e * EG) / GS) * 2u : OOB;
+    sv = buf_load16(rs, so, 0u);
+    bv = buf_load16(rb, so, 0u);
   };
-  auto stash = [&](int buf) {
+  auto stash = [&](const u32x4_t (&xv)[XL], const uint32_t (&wv)[WPT], uint32_t sv, uint32_t bv, int buf) {
 #pragma unroll
     for (int i = 0; i < XL; i++) {
-      const int c = tid + 256 * i;
-      *reinterpret_cast<u32x4_t*>(&xs[buf][(c / 8) * PITCH + 8 * (c % 8)]) = xr[i];
+      const int c = tid + 256 * i, row = c / 8, unit = c % 8;
+      *reinterpret_cast<u32x4_t*>(&xs[buf][row * PITCH + 8 * unit]) = permute8<CO::ORDER>(xv[i]);
+      // the run's sum over the group part (units of a part are adjacent lanes)
+      float t = 0.f;
+#pragma unroll
+      for (int p = 0; p < 4; p++)
+        t += Conv<T>::from_bits(xv[i][p] & 0xffffu) + Conv<T>::from_bits(xv[i][p] >> 16);
+      t += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0xB1, 0xF, 0xF, true));  // quad_perm [1,0,3,2]
+      t += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0x4E, 0xF, 0xF, true));  // quad_perm [2,3,0,1]
+      if constexpr (EG == 64)
+        t += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0x141, 0xF, 0xF, true));  // row_half_mirror
+      if (unit % (EG / 8) == 0) xsum[buf][unit / (EG / 8)][row] = t;
     }
+    const uint32_t magic = opaque(Mma<T>::MAGIC);
 #pragma unroll
-    for (int i = 0; i < WL; i++) {
-      const int c = tid + 256 * i, r = c / (CW / 4), q = c % (CW / 4);
-      if (WCH % 256 != 0 && c >= WCH) continue;
-      const float sc = Conv<T>::from_bits(sr[i]), bi = Conv<T>::from_bits(br[i]);
-      constexpr int VPW = 32 / BITS;  // values per word
-      uint16_t* dh = &ws[buf][0][r * PITCH + q * 4 * VPW];
-      uint16_t* dl = &ws[buf][1][r * PITCH + q * 4 * VPW];
-#pragma unroll
-      for (int j = 0; j < (BITS == 4 ? 4 : 2); j++) {
-        u32x4_t hv, lv;
-        if constexpr (BITS == 4)
-          dequant8<T, 4>(wr[i][j], 0u, sc, bi, hv, lv);
-        else
-          dequant8<T, 8>(wr[i][2 * j], wr[i][2 * j + 1], sc, bi, hv, lv);
-        *reinterpret_cast<u32x4_t*>(dh + 8 * j) = hv;
-        *reinterpret_cast<u32x4_t*>(dl + 8 * j) = lv;
-      }
+    for (int u = 0; u < UPT; u++) {
+      u32x4_t op;
+      if constexpr (BITS == 4)
+        op = CodeOps<T, 4>::operand(wv[u], magic);
+      else
+        op = CodeOps<T, BITS>::operand(wv[2 * u], wv[2 * u + 1]);
+      *reinterpret_cast<u32x4_t*>(&wc[buf][wr_row * PITCH + 8 * (wr_q / UW + u)]) = op;
+    }
+    if (sb_act) {
+      const float sc = Conv<T>::from_bits(sv), bi = Conv<T>::from_bits(bv);
+      sbl[buf][sb_e][sb_row] = make_float2(sc, bi - OFF * sc);
     }
   };
 
@@ -366,36 +391,78 @@ __global__ void __launch_bounds__(256) qmm_lds_kernel(const uint16_t* __restrict
 #pragma unroll
       for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
 
-  const int KT = K / BK;
-  load(0);
-  stash(0);
-  __syncthreads();
-  const int lr = lane & 31, lk = 8 * (lane >> 5);
-  for (int kt = 0; kt < KT; kt++) {
-    const int buf = kt & 1;
-    if (kt + 1 < KT) load(kt + 1);
+  const int lr = lane & 31, lh = lane >> 5;
+  auto compute = [&](int buf) {
 #pragma unroll
-    for (int ks = 0; ks < BK / 16; ks++) {
-      u32x4_t a[TM], bh[TN], bl[TN];
+    for (int e = 0; e < NGK; e++) {
+      f32x16_t d[TM][TN];
 #pragma unroll
-      for (int i = 0; i < TM; i++)
-        a[i] = *reinterpret_cast<const u32x4_t*>(&xs[buf][(wm * WM + 32 * i + lr) * PITCH + 16 * ks + lk]);
+      for (int ss = 0; ss < SPG; ss++) {
+        const int kk = 16 * (e * SPG + ss) + 8 * lh;
+        u32x4_t a[TM], b[TN];
 #pragma unroll
-      for (int j = 0; j < TN; j++) {
-        bh[j] = *reinterpret_cast<const u32x4_t*>(&ws[buf][0][(wn * WN + 32 * j + lr) * PITCH + 16 * ks + lk]);
-        bl[j] = *reinterpret_cast<const u32x4_t*>(&ws[buf][1][(wn * WN + 32 * j + lr) * PITCH + 16 * ks + lk]);
+        for (int i = 0; i < TM; i++)
+          a[i] = *reinterpret_cast<const u32x4_t*>(&xs[buf][(wm * WM + 32 * i + lr) * PITCH + kk]);
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+          b[j] = *reinterpret_cast<const u32x4_t*>(&wc[buf][(wn * WN + 32 * j + lr) * PITCH + kk]);
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+          for (int j = 0; j < TN; j++) {
+            if (ss == 0) {
+              f32x16_t z;
+#pragma unroll
+              for (int v = 0; v < 16; v++) z[v] = 0.f;
+              d[i][j] = mma32<T>(a[i], b[j], z);
+            } else {
+              d[i][j] = mma32<T>(a[i], b[j], d[i][j]);
+            }
+          }
       }
+      // fold the part: lane column n = wn WN + 32 j + lr, rows 8 (v/4) + 4 lh + v%4
+      float2 sb[TN];
 #pragma unroll
-      for (int i = 0; i < TM; i++)
+      for (int j = 0; j < TN; j++) sb[j] = sbl[buf][e][wn * WN + 32 * j + lr];
 #pragma unroll
-        for (int j = 0; j < TN; j++) acc[i][j] = mma32<T>(a[i], bl[j], mma32<T>(a[i], bh[j], acc[i][j]));
+      for (int i = 0; i < TM; i++) {
+        float xsv[16];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const float4 v4 = *reinterpret_cast<const float4*>(&xsum[buf][e][wm * WM + 32 * i + 8 * q + 4 * lh]);
+          xsv[4 * q] = v4.x;
+          xsv[4 * q + 1] = v4.y;
+          xsv[4 * q + 2] = v4.z;
+          xsv[4 * q + 3] = v4.w;
+        }
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+          for (int v = 0; v < 16; v++)
+            acc[i][j][v] = __builtin_fmaf(sb[j].x, d[i][j][v], __builtin_fmaf(sb[j].y, xsv[v], acc[i][j][v]));
+      }
     }
-    if (kt + 1 < KT) stash(buf ^ 1);
-    __syncthreads();
+  };
+
+#pragma unroll
+  for (int p = 0; p < PF; p++) load(kb + p, xr[p], wr[p], sr[p], br[p]);
+  stash(xr[0], wr[0], sr[0], br[0], 0);
+  __syncthreads();
+  for (int k0 = kb; k0 < ke; k0 += PF) {
+#pragma unroll
+    for (int j = 0; j < PF; j++) {
+      const int kt = k0 + j;
+      if (kt < ke) {  // workgroup-uniform
+        const int buf = (kt - kb) & 1;
+        load(kt + PF, xr[j], wr[j], sr[j], br[j]);  // slot j was staged for step kt
+        compute(buf);
+        if (kt + 1 < ke) stash(xr[(j + 1) % PF], wr[(j + 1) % PF], sr[(j + 1) % PF], br[(j + 1) % PF], buf ^ 1);
+        __syncthreads();
+      }
+    }
   }
 
   // D[32 x 32]: lane holds column lane % 32, rows 8 (v / 4) + 4 (lane / 32) + v % 4
-  uint16_t* yb = y + (int64_t)bidx * M * N;
 #pragma unroll
   for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -403,30 +470,81 @@ __global__ void __launch_bounds__(256) qmm_lds_kernel(const uint16_t* __restrict
       const int n = n0 + wn * WN + 32 * j + lr;
 #pragma unroll
       for (int v = 0; v < 16; v++) {
-        const int m = m0 + wm * WM + 32 * i + 8 * (v / 4) + 4 * (lane >> 5) + v % 4;
-        if (m < M && n < N) yb[(int64_t)m * N + n] = (uint16_t)Conv<T>::to_bits(acc[i][j][v]);
+        const int m = m0 + wm * WM + 32 * i + 8 * (v / 4) + 4 * lh + v % 4;
+        if (m < M && n < N) {
+          if (KS == 1)
+            y[((int64_t)bidx * M + m) * N + n] = (uint16_t)Conv<T>::to_bits(acc[i][j][v]);
+          else
+            part[(((int64_t)split * gridDim.z / KS + bidx) * M + m) * N + n] = acc[i][j][v];
+        }
       }
     }
 }
 
-template <typename T, int BITS, int GS>
-int launch_qmm_lds(const void* x, int64_t batch, int64_t M, int64_t K, const uint32_t* w, const void* scales,
-                   const void* biases, int64_t w_rep, int64_t N, void* y, hipStream_t s) {
-#define QMM_L(BMV, BNV)                                                                                          \
-  {                                                                                                              \
-    dim3 grid((unsigned)((N + BNV - 1) / BNV), (unsigned)((M + BMV - 1) / BMV), (unsigned)batch);              \
-    hipLaunchKernelGGL((qmm_lds_kernel<T, BITS, GS, BMV, BNV>), grid, dim3(256), 0, s, (const uint16_t*)x, (int)M, \
-                       (int)K, w, (const uint16_t*)scales, (const uint16_t*)biases, (int)N, (int)w_rep,          \
-                       (uint16_t*)y);                                                                            \
+// y = T(sum over splits of the fp32 partials), fixed split order.
+template <typename T>
+__global__ void __launch_bounds__(256) qmm_splitk_reduce_kernel(const float4* __restrict__ part, int64_t n4, int KS,
+                                                                uint2* __restrict__ y) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n4) return;
+  float4 a = part[i];
+  for (int k = 1; k < KS; k++) {
+    const float4 b = part[(int64_t)k * n4 + i];
+    a.x += b.x;
+    a.y += b.y;
+    a.z += b.z;
+    a.w += b.w;
   }
-  // big tiles once they still give every CU a workgroup
-  if (M >= 128 && ((N + 127) / 128) * ((M + 127) / 128) * batch >= mlxq::device_cu_count())
-    QMM_L(128, 128)
-  else
-    QMM_L(64, 64)
-#undef QMM_L
-  MLXQ_LAUNCHED("qmm_lds_kernel");
+  y[i] = make_uint2(Conv<T>::to_bits(a.x) | (Conv<T>::to_bits(a.y) << 16),
+                    Conv<T>::to_bits(a.z) | (Conv<T>::to_bits(a.w) << 16));
+}
+
+// Tile and split choice: BM 32 for M <= 32 (weight-stream bound, 128-wide
+// tiles), 64 x 64 up to M = 96, 128 x 128 once those give every CU a
+// workgroup; K is split (fp32 partials + reduce) until about two workgroups
+// per CU, keeping at least 8 K-steps per split.
+template <typename T, int BITS, int GS, int BM, int BN>
+int launch_qmm_tile_inst(const void* x, int64_t batch, int64_t M, int64_t K, const uint32_t* w, const void* scales,
+                         const void* biases, int64_t w_rep, int64_t N, void* y, hipStream_t s) {
+  const int64_t tiles = ((N + BN - 1) / BN) * ((M + BM - 1) / BM) * batch;
+  const int64_t KT = K / 64;
+  const int64_t target = 2 * (int64_t)mlxq::device_cu_count();
+  int KS = 1;
+  const bool can_split = N % 4 == 0 && (uintptr_t)y % 8 == 0;
+  while (can_split && KS < 64 && tiles * KS * 2 <= target && KT / (KS * 2) >= 8) KS *= 2;
+  const size_t pbytes = KS > 1 ? (size_t)KS * batch * M * N * sizeof(float) : 0;
+  float* part = nullptr;
+  if (pbytes) {
+    uint32_t* unused_counters = nullptr;
+    void* p = nullptr;
+    int rc = mlxq::workspace(pbytes, 0, &unused_counters, &p, s);
+    if (rc) return rc;
+    part = (float*)p;
+  }
+  const int KTS = (int)((KT + KS - 1) / KS);
+  MLXQ_CHECK(batch * KS < 65536, "qmm: batch too large for one launch");
+  dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM), (unsigned)(batch * KS));
+  hipLaunchKernelGGL((qmm_tile_kernel<T, BITS, GS, BM, BN>), grid, dim3(256), 0, s, (const uint16_t*)x, (int)M,
+                     (int)K, w, (const uint16_t*)scales, (const uint16_t*)biases, (int)N, (int)w_rep, KS, KTS,
+                     (uint16_t*)y, part);
+  MLXQ_LAUNCHED("qmm_tile_kernel");
+  if (KS > 1) {
+    const int64_t n4 = batch * M * N / 4;
+    hipLaunchKernelGGL((qmm_splitk_reduce_kernel<T>), dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s,
+                       (const float4*)part, n4, KS, (uint2*)y);
+    MLXQ_LAUNCHED("qmm_splitk_reduce_kernel");
+  }
   return MLXQ_OK;
+}
+
+template <typename T, int BITS, int GS>
+int launch_qmm_tile(const void* x, int64_t batch, int64_t M, int64_t K, const uint32_t* w, const void* scales,
+                    const void* biases, int64_t w_rep, int64_t N, void* y, hipStream_t s) {
+  if (M <= 32)
+    return launch_qmm_tile_inst<T, BITS, GS, 32, 128>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);
+  if (M >= 128 && ((N + 127) / 128) * ((M + 127) / 128) * batch >= mlxq::device_cu_count())
+    return launch_qmm_tile_inst<T, BITS, GS, 128, 128>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);
+  return launch_qmm_tile_inst<T, BITS, GS, 64, 64>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);
 }
 
 // ---- generic VALU path -----------------------------------------------------
@@ -603,25 +721,25 @@ extern "C" int mlxq_quantized_matmul(const void* x, int dtype, int64_t batch, in
                             : launch_qmv<F16, 8, 128>(x, batch, M, K, w, scales, biases, w_rep, N, y, plan, s);
   }
 
-  const bool lds_ok = transpose && mlxq::is_half_dtype(dtype) && (bits == 4 || bits == 8) && K % 64 == 0 &&
+  const bool tile_ok = transpose && mlxq::is_half_dtype(dtype) && (bits == 4 || bits == 8) && K % 64 == 0 &&
                       (uintptr_t)x % 16 == 0 && (uintptr_t)w % 16 == 0 && (uintptr_t)scales % 2 == 0 &&
                       M * K * 2 < ((int64_t)1 << 31) && N * K < ((int64_t)1 << 31);
-  if (lds_ok) {
-#define QMM_LDS_T(TT)                                                                                           \
+  if (tile_ok) {
+#define QMM_TILE_T(TT)                                                                                           \
   switch (bits * 1000 + group_size) {                                                                           \
-    case 4032: return launch_qmm_lds<TT, 4, 32>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);             \
-    case 4064: return launch_qmm_lds<TT, 4, 64>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);             \
-    case 4128: return launch_qmm_lds<TT, 4, 128>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);            \
-    case 8032: return launch_qmm_lds<TT, 8, 32>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);             \
-    case 8064: return launch_qmm_lds<TT, 8, 64>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);             \
-    default: return launch_qmm_lds<TT, 8, 128>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);              \
+    case 4032: return launch_qmm_tile<TT, 4, 32>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);            \
+    case 4064: return launch_qmm_tile<TT, 4, 64>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);            \
+    case 4128: return launch_qmm_tile<TT, 4, 128>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);           \
+    case 8032: return launch_qmm_tile<TT, 8, 32>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);            \
+    case 8064: return launch_qmm_tile<TT, 8, 64>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);            \
+    default: return launch_qmm_tile<TT, 8, 128>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);             \
   }
     if (dtype == MLXQ_BFLOAT16) {
-      QMM_LDS_T(BF16)
+      QMM_TILE_T(BF16)
     } else {
-      QMM_LDS_T(F16)
+      QMM_TILE_T(F16)
     }
-#undef QMM_LDS_T
+#undef QMM_TILE_T
   }
 
   const int64_t outs = M * N;

@@ -105,3 +105,23 @@ def test_qmm_batched_broadcast(O, mlxq_dev):
                             DeviceArray.fromNumpy(s, BF16), DeviceArray.fromNumpy(b, BF16), ops.QuantSpec(bits, gs))
     ref = O.qmm(x.reshape(8, 3, 128), p.reshape(2, 40, 16), s.reshape(2, 40, 2), b.reshape(2, 40, 2), gs, bits, BF16)
     assert_close(y.toFloat32().reshape(8, 3, 40), ref, what="batched", dtype=BF16)
+
+
+@pytest.mark.parametrize("dtype,bits,gs,lead,M,N,K", [
+    (BF16, 4, 32, (), 24, 300, 4096),     # 32 x 128 tiles, K split 8 ways
+    (F16, 8, 128, (), 40, 264, 2048),     # 64 x 64 tiles, a K-step is half a group
+    (BF16, 8, 64, (), 130, 512, 1024),    # ragged M tiles
+    (F16, 4, 64, (), 20, 77, 8192),       # N % 4 != 0: one split over a long K
+    (BF16, 4, 64, (3,), 33, 96, 2048),    # batch 3 against one broadcast w, split K
+    (BF16, 4, 128, (), 512, 8192, 512),   # 128 x 128 tiles
+    (F16, 8, 32, (), 100, 136, 3072),     # two group parts per K-step, split K
+])
+def test_qmm_tile(O, mlxq_dev, dtype, bits, gs, lead, M, N, K):
+    """The tiled MFMA GEMM (M beyond qmv, or K too long for qmv's x slices):
+    every bits / group_size / dtype pairing, split-K partials and the
+    reduce, tiles cut by M and N."""
+    w = rng_t(O, (N, K), 11, dtype, 0.05)
+    wq = O.quantize(w, gs, bits, dtype)
+    x = rng_t(O, lead + (M, K), 12, dtype)
+    y = run_qmm(O, mlxq_dev, x, wq, gs, bits, dtype)
+    assert_close(y, x.astype(np.float64) @ deq64(O, *wq, gs, bits, dtype).T, what="tile", dtype=dtype)
