@@ -85,6 +85,17 @@ __device__ __forceinline__ uint32_t buf_load16(__amdgpu_buffer_rsrc_t r, uint32_
   return __builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, (int)soff, 0);
 }
 
+// Workgroup barrier that orders LDS only.  __syncthreads() also orders
+// global memory, which compiles to s_waitcnt vmcnt(0) before s_barrier: every
+// wave would wait for all of its outstanding global loads, draining any
+// register prefetch carried across the barrier.  Here only LDS accesses
+// (lgkmcnt) are completed first.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 // v_mfma_f32_32x32x16_{bf16,f16}: A [32 x 16] lane l = row l % 32, k slots

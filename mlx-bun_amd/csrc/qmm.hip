@@ -215,13 +215,13 @@ __global__ void __launch_bounds__(512) qmv_kernel(const uint16_t* __restrict__ x
   }
 
   // ---- 5. reduce the waves (fixed order) and store --------------------------
-  __syncthreads();  // every wave is done with its LDS region
+  lds_barrier();  // every wave is done with its LDS region
   f32x4_t* red = reinterpret_cast<f32x4_t*>(smem);  // [nw][R * MB][64]
 #pragma unroll
   for (int ri = 0; ri < R; ri++)
 #pragma unroll
     for (int rb = 0; rb < MB; rb++) red[(wave * R * MB + ri * MB + rb) * 64 + lane] = yacc[ri][rb];
-  __syncthreads();
+  lds_barrier();
   if (wave < R * MB) {
     const int ri = wave / MB, rb = wave % MB;
     f32x4_t acc = red[wave * 64 + lane];
@@ -252,12 +252,12 @@ __global__ void __launch_bounds__(512) qmv_kernel(const uint16_t* __restrict__ x
 //   * the x tile as T, each 8-value run permuted into the code slot order;
 //   * the weight codes as exact MFMA operands OFF + c (CodeOps);
 //   * per part of a quant group inside the step (64 values, or 32 for
-//     group_size 32): every weight row's (s, b - OFF s) and every x row's
-//     sum X of the run.
-// The 32x32x16 MFMAs contract one group part at a time into D, and the part
-// folds into the fp32 accumulators as acc += s D + (b - OFF s) X: the products
-// are exact and only fp32 accumulation rounds, so no rounding of dequantized
-// weights to T enters the result.
+//     group_size 32): every weight row's (s, b - OFF s).
+// The 32x32x16 MFMAs contract one group part at a time into D (x against the
+// codes) and X (x against ones: the row sums of x, already in D's layout),
+// and the part folds into the fp32 accumulators as acc += s D + (b - OFF s) X:
+// the products are exact and only fp32 accumulation rounds, so no rounding of
+// dequantized weights to T enters the result.
 // Register prefetch runs PF K-steps ahead of the LDS double buffer (one
 // barrier per step).  Workgroups of a split K (blockIdx.z = batch * KS +
 // split) write fp32 partials that qmm_splitk_reduce_kernel sums in fixed
@@ -277,8 +277,8 @@ __global__ void __launch_bounds__(256) qmm_tile_kernel(const uint16_t* __restric
                                                        const uint32_t* __restrict__ w,
                                                        const uint16_t* __restrict__ scales,
                                                        const uint16_t* __restrict__ biases, int N, int w_rep,
-                                                       int KS, int KTS, uint16_t* __restrict__ y,
-                                                       float* __restrict__ part) {
+                                                       int KS, int KTS, uint32_t sb_bytes,
+                                                       uint16_t* __restrict__ y, float* __restrict__ part) {
   using SH = TileShape<BM, BN>;
   using CO = CodeOps<T, BITS>;
   constexpr int WM = SH::WM, WN = SH::WN, TM = SH::TM, TN = SH::TN, PF = SH::PF;
@@ -298,7 +298,6 @@ __global__ void __launch_bounds__(256) qmm_tile_kernel(const uint16_t* __restric
   __shared__ __align__(16) uint16_t xs[2][BM * PITCH];
   __shared__ __align__(16) uint16_t wc[2][BN * PITCH];
   __shared__ __align__(16) float2 sbl[2][NGK][BN];
-  __shared__ __align__(16) float xsum[2][NGK][BM];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / SH::WGN, wn = wave % SH::WGN;
@@ -310,8 +309,12 @@ __global__ void __launch_bounds__(256) qmm_tile_kernel(const uint16_t* __restric
   const int mrows = min(BM, M - m0), nrows = min(BN, N - n0);
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + ((int64_t)bidx * M + m0) * K, (uint32_t)(mrows * K * 2));
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(w + ((int64_t)wb * N + n0) * (row_bytes / 4), (uint32_t)nrows * row_bytes);
-  const __amdgpu_buffer_rsrc_t rs = make_rsrc(scales + ((int64_t)wb * N + n0) * G, (uint32_t)(nrows * G * 2));
-  const __amdgpu_buffer_rsrc_t rb = make_rsrc(biases + ((int64_t)wb * N + n0) * G, (uint32_t)(nrows * G * 2));
+  // scales / biases: whole arrays (4-byte aligned), read as the dword that
+  // holds the wanted 16-bit value (a 16-bit load feeding the prefetch ring
+  // would be widened, and so waited for, right at the load)
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(scales, sb_bytes);
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(biases, sb_bytes);
+  const int64_t sb_elem0 = ((int64_t)wb * N + n0) * G;  // tile's first (row, group) element
   constexpr uint32_t OOB = 0x80000000u;  // past every descriptor: reads 0
 
   // thread -> staging items.  x: chunk c = tid + 256 i -> row c / 8, unit
@@ -324,48 +327,46 @@ __global__ void __launch_bounds__(256) qmm_tile_kernel(const uint16_t* __restric
   u32x4_t xr[PF][XL];
   uint32_t wr[PF][WPT];
   uint32_t sr[PF], br[PF];
+  // element index of (row sb_row, group of part sb_e) in K-step kt
+  auto sb_elem = [&](int kt) -> int64_t {
+    return sb_elem0 + (int64_t)sb_row * G + ((int64_t)kt * BK + sb_e * EG) / GS;
+  };
+  // Steps past the split's end re-read its last step (never staged): a
+  // masked offset would be a uniform select, which the compiler turns into
+  // branches whose loads wait for the whole prefetch ring.
   auto load = [&](int kt, u32x4_t (&xv)[XL], uint32_t (&wv)[WPT], uint32_t& sv, uint32_t& bv) {
-    const bool ok = kt < ke;
+    kt = min(kt, ke - 1);
     const uint32_t k0 = (uint32_t)kt * BK;
 #pragma unroll
     for (int i = 0; i < XL; i++) {
       const int c = tid + 256 * i;
-      xv[i] = buf_load128(rx, ok ? ((uint32_t)(c / 8) * (uint32_t)K + k0 + 8u * (c % 8)) * 2u : OOB, 0u);
+      xv[i] = buf_load128(rx, ((uint32_t)(c / 8) * (uint32_t)K + 8u * (c % 8)) * 2u, k0 * 2u);
     }
-    const uint32_t wo = ok ? (uint32_t)wr_row * row_bytes + k0 * BITS / 8 + 4u * wr_q : OOB;
+    const uint32_t wo = (uint32_t)wr_row * row_bytes + 4u * wr_q;
     if constexpr (WPT == 2) {
-      const auto v = __builtin_amdgcn_raw_buffer_load_b64(rw, (int)wo, 0, 0);
+      const auto v = __builtin_amdgcn_raw_buffer_load_b64(rw, (int)wo, (int)(k0 * BITS / 8), 0);
       wv[0] = v[0];
       wv[1] = v[1];
     } else {
 #pragma unroll
       for (int h = 0; h < WPT / 4; h++) {
-        const u32x4_t v = buf_load128(rw, wo + 16u * h, 0u);
+        const u32x4_t v = buf_load128(rw, wo + 16u * h, k0 * BITS / 8);
         wv[4 * h] = v.x;
         wv[4 * h + 1] = v.y;
         wv[4 * h + 2] = v.z;
         wv[4 * h + 3] = v.w;
       }
     }
-    const uint32_t so = (ok && sb_act) ? ((uint32_t)sb_row * (uint32_t)G + (k0 + (uint32_t)sb_e * EG) / GS) * 2u : OOB;
-    sv = buf_load16(rs, so, 0u);
-    bv = buf_load16(rb, so, 0u);
+    const uint32_t so = sb_act ? (uint32_t)(2 * sb_elem(kt)) & ~3u : OOB;
+    sv = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)so, 0, 0);
+    bv = __builtin_amdgcn_raw_buffer_load_b32(rb, (int)so, 0, 0);
   };
-  auto stash = [&](const u32x4_t (&xv)[XL], const uint32_t (&wv)[WPT], uint32_t sv, uint32_t bv, int buf) {
+  auto stash = [&](const u32x4_t (&xv)[XL], const uint32_t (&wv)[WPT], uint32_t sv, uint32_t bv, int kt,
+                   int buf) {
 #pragma unroll
     for (int i = 0; i < XL; i++) {
       const int c = tid + 256 * i, row = c / 8, unit = c % 8;
       *reinterpret_cast<u32x4_t*>(&xs[buf][row * PITCH + 8 * unit]) = permute8<CO::ORDER>(xv[i]);
-      // the run's sum over the group part (units of a part are adjacent lanes)
-      float t = 0.f;
-#pragma unroll
-      for (int p = 0; p < 4; p++)
-        t += Conv<T>::from_bits(xv[i][p] & 0xffffu) + Conv<T>::from_bits(xv[i][p] >> 16);
-      t += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0xB1, 0xF, 0xF, true));  // quad_perm [1,0,3,2]
-      t += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0x4E, 0xF, 0xF, true));  // quad_perm [2,3,0,1]
-      if constexpr (EG == 64)
-        t += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0x141, 0xF, 0xF, true));  // row_half_mirror
-      if (unit % (EG / 8) == 0) xsum[buf][unit / (EG / 8)][row] = t;
     }
     const uint32_t magic = opaque(Mma<T>::MAGIC);
 #pragma unroll
@@ -378,7 +379,8 @@ __global__ void __launch_bounds__(256) qmm_tile_kernel(const uint16_t* __restric
       *reinterpret_cast<u32x4_t*>(&wc[buf][wr_row * PITCH + 8 * (wr_q / UW + u)]) = op;
     }
     if (sb_act) {
-      const float sc = Conv<T>::from_bits(sv), bi = Conv<T>::from_bits(bv);
+      const int sh = 16 * (int)(sb_elem(kt) & 1);
+      const float sc = Conv<T>::from_bits((sv >> sh) & 0xffffu), bi = Conv<T>::from_bits((bv >> sh) & 0xffffu);
       sbl[buf][sb_e][sb_row] = make_float2(sc, bi - OFF * sc);
     }
   };
@@ -392,10 +394,37 @@ __global__ void __launch_bounds__(256) qmm_tile_kernel(const uint16_t* __restric
       for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
 
   const int lr = lane & 31, lh = lane >> 5;
+  const u32x4_t ones = {Mma<T>::ONES, Mma<T>::ONES, Mma<T>::ONES, Mma<T>::ONES};
+  // A group part's fold is deferred until the next part's MFMAs are issued
+  // (where registers allow), so its VALU work overlaps the matrix core; the
+  // pending part starts as zeros (folding it adds nothing).
+  constexpr bool DEFER = TM * TN <= 2;
+  f32x16_t pd[DEFER ? TM : 1][DEFER ? TN : 1], px[DEFER ? TM : 1];
+  float2 psb[DEFER ? TN : 1];
+#pragma unroll
+  for (int i = 0; i < (DEFER ? TM : 1); i++) {
+#pragma unroll
+    for (int v = 0; v < 16; v++) px[i][v] = 0.f;
+#pragma unroll
+    for (int j = 0; j < (DEFER ? TN : 1); j++)
+#pragma unroll
+      for (int v = 0; v < 16; v++) pd[i][j][v] = 0.f;
+  }
+#pragma unroll
+  for (int j = 0; j < (DEFER ? TN : 1); j++) psb[j] = make_float2(0.f, 0.f);
+  auto fold = [&](const f32x16_t (&d)[TM][TN], const f32x16_t (&xsm)[TM], const float2 (&sb)[TN]) {
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int j = 0; j < TN; j++)
+#pragma unroll
+        for (int v = 0; v < 16; v++)
+          acc[i][j][v] = __builtin_fmaf(sb[j].x, d[i][j][v], __builtin_fmaf(sb[j].y, xsm[i][v], acc[i][j][v]));
+  };
   auto compute = [&](int buf) {
 #pragma unroll
     for (int e = 0; e < NGK; e++) {
-      f32x16_t d[TM][TN];
+      f32x16_t d[TM][TN], xsm[TM];
 #pragma unroll
       for (int ss = 0; ss < SPG; ss++) {
         const int kk = 16 * (e * SPG + ss) + 8 * lh;
@@ -406,61 +435,59 @@ __global__ void __launch_bounds__(256) qmm_tile_kernel(const uint16_t* __restric
 #pragma unroll
         for (int j = 0; j < TN; j++)
           b[j] = *reinterpret_cast<const u32x4_t*>(&wc[buf][(wn * WN + 32 * j + lr) * PITCH + kk]);
+        f32x16_t z;
 #pragma unroll
-        for (int i = 0; i < TM; i++)
+        for (int v = 0; v < 16; v++) z[v] = 0.f;
 #pragma unroll
-          for (int j = 0; j < TN; j++) {
-            if (ss == 0) {
-              f32x16_t z;
+        for (int i = 0; i < TM; i++) {
+          xsm[i] = mma32<T>(a[i], ones, ss == 0 ? z : xsm[i]);
 #pragma unroll
-              for (int v = 0; v < 16; v++) z[v] = 0.f;
-              d[i][j] = mma32<T>(a[i], b[j], z);
-            } else {
-              d[i][j] = mma32<T>(a[i], b[j], d[i][j]);
-            }
-          }
+          for (int j = 0; j < TN; j++) d[i][j] = mma32<T>(a[i], b[j], ss == 0 ? z : d[i][j]);
+        }
       }
-      // fold the part: lane column n = wn WN + 32 j + lr, rows 8 (v/4) + 4 lh + v%4
+      // fold: lane column n = wn WN + 32 j + lr, rows 8 (v/4) + 4 lh + v%4
       float2 sb[TN];
 #pragma unroll
       for (int j = 0; j < TN; j++) sb[j] = sbl[buf][e][wn * WN + 32 * j + lr];
+      if constexpr (DEFER) {
+        fold(pd, px, psb);
 #pragma unroll
-      for (int i = 0; i < TM; i++) {
-        float xsv[16];
+        for (int i = 0; i < TM; i++) {
+          px[i] = xsm[i];
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-          const float4 v4 = *reinterpret_cast<const float4*>(&xsum[buf][e][wm * WM + 32 * i + 8 * q + 4 * lh]);
-          xsv[4 * q] = v4.x;
-          xsv[4 * q + 1] = v4.y;
-          xsv[4 * q + 2] = v4.z;
-          xsv[4 * q + 3] = v4.w;
+          for (int j = 0; j < TN; j++) pd[i][j] = d[i][j];
         }
 #pragma unroll
-        for (int j = 0; j < TN; j++)
-#pragma unroll
-          for (int v = 0; v < 16; v++)
-            acc[i][j][v] = __builtin_fmaf(sb[j].x, d[i][j][v], __builtin_fmaf(sb[j].y, xsv[v], acc[i][j][v]));
+        for (int j = 0; j < TN; j++) psb[j] = sb[j];
+      } else {
+        fold(d, xsm, sb);
       }
     }
   };
 
 #pragma unroll
   for (int p = 0; p < PF; p++) load(kb + p, xr[p], wr[p], sr[p], br[p]);
-  stash(xr[0], wr[0], sr[0], br[0], 0);
-  __syncthreads();
+  stash(xr[0], wr[0], sr[0], br[0], kb, 0);
+  lds_barrier();
+  // Loads are unconditional (steps past the end re-read the last one) so the
+  // count of loads between any two points is static and the waits before a
+  // stash leave the later slots in flight.
   for (int k0 = kb; k0 < ke; k0 += PF) {
 #pragma unroll
     for (int j = 0; j < PF; j++) {
       const int kt = k0 + j;
+      load(kt + PF, xr[j], wr[j], sr[j], br[j]);  // slot j was staged for step kt
       if (kt < ke) {  // workgroup-uniform
         const int buf = (kt - kb) & 1;
-        load(kt + PF, xr[j], wr[j], sr[j], br[j]);  // slot j was staged for step kt
         compute(buf);
-        if (kt + 1 < ke) stash(xr[(j + 1) % PF], wr[(j + 1) % PF], sr[(j + 1) % PF], br[(j + 1) % PF], buf ^ 1);
-        __syncthreads();
+        if (kt + 1 < ke)
+          stash(xr[(j + 1) % PF], wr[(j + 1) % PF], sr[(j + 1) % PF], br[(j + 1) % PF], kt + 1, buf ^ 1);
+        lds_barrier();
       }
     }
   }
+
+  if constexpr (DEFER) fold(pd, px, psb);
 
   // D[32 x 32]: lane holds column lane % 32, rows 8 (v / 4) + 4 (lane / 32) + v % 4
 #pragma unroll
@@ -488,30 +515,50 @@ __global__ void __launch_bounds__(256) qmm_splitk_reduce_kernel(const float4* __
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= n4) return;
   float4 a = part[i];
-  for (int k = 1; k < KS; k++) {
-    const float4 b = part[(int64_t)k * n4 + i];
-    a.x += b.x;
-    a.y += b.y;
-    a.z += b.z;
-    a.w += b.w;
+  for (int k0 = 1; k0 < KS; k0 += 8) {
+    float4 b[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) b[k] = k0 + k < KS ? part[(int64_t)(k0 + k) * n4 + i] : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      a.x += b[k].x;
+      a.y += b[k].y;
+      a.z += b[k].z;
+      a.w += b[k].w;
+    }
   }
   y[i] = make_uint2(Conv<T>::to_bits(a.x) | (Conv<T>::to_bits(a.y) << 16),
                     Conv<T>::to_bits(a.z) | (Conv<T>::to_bits(a.w) << 16));
 }
 
-// Tile and split choice: BM 32 for M <= 32 (weight-stream bound, 128-wide
-// tiles), 64 x 64 up to M = 96, 128 x 128 once those give every CU a
-// workgroup; K is split (fp32 partials + reduce) until about two workgroups
-// per CU, keeping at least 8 K-steps per split.
+// Tile and split choice: 32 x 128 for M <= 32 and 64 x 128 for M <= 64
+// (x staging amortised over 128 weight rows), 128 x 128 once those give every
+// CU a workgroup, else 64 x 64; K is split (fp32 partials + reduce) until every CU
+// has a workgroup, keeping at least 8 K-steps per split.
+inline int64_t w_batch_of(int64_t batch, int64_t w_rep) { return batch / w_rep; }
+
+// MLXQ_QMM_KS: fixed K split (power of two) for the tiled GEMM (tuning)
+int qmm_ks_override() {
+  static const int v = [] {
+    const char* e = getenv("MLXQ_QMM_KS");
+    return e ? atoi(e) : 0;
+  }();
+  return v;
+}
+
 template <typename T, int BITS, int GS, int BM, int BN>
 int launch_qmm_tile_inst(const void* x, int64_t batch, int64_t M, int64_t K, const uint32_t* w, const void* scales,
                          const void* biases, int64_t w_rep, int64_t N, void* y, hipStream_t s) {
   const int64_t tiles = ((N + BN - 1) / BN) * ((M + BM - 1) / BM) * batch;
   const int64_t KT = K / 64;
-  const int64_t target = 2 * (int64_t)mlxq::device_cu_count();
+  const int64_t target = mlxq::device_cu_count();
   int KS = 1;
   const bool can_split = N % 4 == 0 && (uintptr_t)y % 8 == 0;
-  while (can_split && KS < 64 && tiles * KS * 2 <= target && KT / (KS * 2) >= 8) KS *= 2;
+  // smallest split that gives every CU a workgroup (more only adds fp32
+  // partial traffic and contention)
+  while (can_split && KS < 64 && tiles * KS < target && KT / (KS * 2) >= 8) KS *= 2;
+  const int ov = qmm_ks_override();
+  if (ov >= 1 && ov <= 64 && (ov == 1 || can_split)) KS = ov;
   const size_t pbytes = KS > 1 ? (size_t)KS * batch * M * N * sizeof(float) : 0;
   float* part = nullptr;
   if (pbytes) {
@@ -526,7 +573,7 @@ int launch_qmm_tile_inst(const void* x, int64_t batch, int64_t M, int64_t K, con
   dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM), (unsigned)(batch * KS));
   hipLaunchKernelGGL((qmm_tile_kernel<T, BITS, GS, BM, BN>), grid, dim3(256), 0, s, (const uint16_t*)x, (int)M,
                      (int)K, w, (const uint16_t*)scales, (const uint16_t*)biases, (int)N, (int)w_rep, KS, KTS,
-                     (uint16_t*)y, part);
+                     (uint32_t)(((w_batch_of(batch, w_rep) * N * (K / GS)) * 2 + 3) & ~(int64_t)3), (uint16_t*)y, part);
   MLXQ_LAUNCHED("qmm_tile_kernel");
   if (KS > 1) {
     const int64_t n4 = batch * M * N / 4;
@@ -544,6 +591,8 @@ int launch_qmm_tile(const void* x, int64_t batch, int64_t M, int64_t K, const ui
     return launch_qmm_tile_inst<T, BITS, GS, 32, 128>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);
   if (M >= 128 && ((N + 127) / 128) * ((M + 127) / 128) * batch >= mlxq::device_cu_count())
     return launch_qmm_tile_inst<T, BITS, GS, 128, 128>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);
+  if (M <= 64)
+    return launch_qmm_tile_inst<T, BITS, GS, 64, 128>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);
   return launch_qmm_tile_inst<T, BITS, GS, 64, 64>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);
 }
 
@@ -722,8 +771,9 @@ extern "C" int mlxq_quantized_matmul(const void* x, int dtype, int64_t batch, in
   }
 
   const bool tile_ok = transpose && mlxq::is_half_dtype(dtype) && (bits == 4 || bits == 8) && K % 64 == 0 &&
-                      (uintptr_t)x % 16 == 0 && (uintptr_t)w % 16 == 0 && (uintptr_t)scales % 2 == 0 &&
-                      M * K * 2 < ((int64_t)1 << 31) && N * K < ((int64_t)1 << 31);
+                      (uintptr_t)x % 16 == 0 && (uintptr_t)w % 16 == 0 && (uintptr_t)scales % 4 == 0 &&
+                      (uintptr_t)biases % 4 == 0 && M * K * 2 < ((int64_t)1 << 31) && N * K < ((int64_t)1 << 31) &&
+                      w_batch * N * (K / group_size) * 2 < ((int64_t)1 << 31);
   if (tile_ok) {
 #define QMM_TILE_T(TT)                                                                                           \
   switch (bits * 1000 + group_size) {                                                                           \

@@ -346,7 +346,7 @@ __global__ void __launch_bounds__(512) sdpa_decode_mfma_kernel(
   qsum = xrow_sum(qsum);
   const uint32_t magic = opaque(Mma<T>::MAGIC);
   const u32x4_t ones = {Mma<T>::ONES, Mma<T>::ONES, Mma<T>::ONES, Mma<T>::ONES};
-  __syncthreads();  // sb_lds ready
+  lds_barrier();  // sb_lds ready
 
   // ---- per-wave online softmax state --------------------------------------
   float m_run = -INFINITY;  // per head h_me (log2 domain), replicated over g and lane rows
@@ -503,7 +503,7 @@ __global__ void __launch_bounds__(512) sdpa_decode_mfma_kernel(
   // ---- wave result: u[h][d] = O - OFF * sp + pb (rows whose group owns d) -
   l_run = xrow_sum(l_run);
   pb_run = xrow_sum(pb_run);
-  __syncthreads();  // every wave is done reading sb_lds, which u_lds overlays
+  lds_barrier();  // every wave is done reading sb_lds, which u_lds overlays
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const int r = 4 * lg + i;
@@ -523,7 +523,7 @@ __global__ void __launch_bounds__(512) sdpa_decode_mfma_kernel(
     m_lds[wave][h_me] = m_run;
     l_lds[wave][h_me] = l_run;
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- merge the waves (fixed order) ---------------------------------------
   const bool single = cr.nch == 1;
@@ -594,7 +594,7 @@ __global__ void __launch_bounds__(256) sdpa_decode_merge_kernel(const float4* __
   }
   ul[wave][lane] = U;
   mll[wave][lane] = make_float2(M, L);
-  __syncthreads();
+  lds_barrier();
   if (wave != 0 || !active) return;
   float Mt = -INFINITY;
 #pragma unroll
@@ -817,7 +817,7 @@ __global__ void __launch_bounds__(512) sdpa_prefill_mfma_kernel(
     load(kbeg);
     stash(0);
   }
-  __syncthreads();
+  lds_barrier();
   int buf = 0;
   for (int64_t k0 = kbeg; k0 < kend; k0 += BN) {
     const bool more = k0 + BN < kend;
@@ -890,7 +890,7 @@ __global__ void __launch_bounds__(512) sdpa_prefill_mfma_kernel(
       }
     }
     if (more) stash(buf ^ 1);
-    __syncthreads();
+    lds_barrier();
     buf ^= 1;
   }
 
