@@ -715,8 +715,9 @@ __global__ void __launch_bounds__(512) sdpa_prefill_mfma_kernel(
   }
 
   // ---- K/V tile loads: item it < KI is (key it / (D/32), 32 codes), else
-  // (4 keys, 8 codes) of V; loads are raw buffer loads bounded to the row's
-  // valid keys (keys past them read 0) ----------------------------------------
+  // (4 keys, 8 codes) of V with the key quad fastest across lanes (the V^T
+  // writes of one instruction then land on distinct LDS banks); loads are
+  // raw buffer loads bounded to the row's valid keys (keys past them read 0)
   const __amdgpu_buffer_rsrc_t rk = make_rsrc(kp + rowbase * KW, (uint32_t)(valid * KW * 4));
   const __amdgpu_buffer_rsrc_t rv = make_rsrc(vp + rowbase * KW, (uint32_t)(valid * KW * 4));
   const __amdgpu_buffer_rsrc_t rks = make_rsrc(ksc + rowbase * G, (uint32_t)(valid * G * 2));
@@ -744,7 +745,7 @@ __global__ void __launch_bounds__(512) sdpa_prefill_mfma_kernel(
         reg_s[u][0] = buf_load16(rks, so, 0u);
         reg_b[u][0] = buf_load16(rkb, so, 0u);
       } else if (it < KI + VI) {
-        const int vi = it - KI, kq = vi / (D / 8), d8 = vi % (D / 8);
+        const int vi = it - KI, kq = vi % (BN / 4), d8 = vi / (BN / 4);
 #pragma unroll
         for (int kk = 0; kk < 4; kk++) {
           const uint32_t roff = (uint32_t)(k0 + 4 * kq + kk) * (uint32_t)(KW * 4) + (uint32_t)d8 * VIW * 4;
@@ -783,7 +784,7 @@ __global__ void __launch_bounds__(512) sdpa_prefill_mfma_kernel(
                                                              Mma<T>::pack2(v[4], v[5]), Mma<T>::pack2(v[6], v[7])};
         }
       } else if (it < KI + VI) {
-        const int vi = it - KI, kq = vi / (D / 8), d8 = vi % (D / 8);
+        const int vi = it - KI, kq = vi % (BN / 4), d8 = vi / (BN / 4);
         float sc[4], bi[4];
 #pragma unroll
         for (int kk = 0; kk < 4; kk++) {

@@ -156,3 +156,23 @@ def test_reference_decode_sites_vs_unfused(O, mlxq_dev, site):
     assert np.abs(got - un).max() < 0.02
     assert np.abs(un).mean() > 0.001
     check(O, got, q, kq, vq, bf, 1.0, gs, bits, "site")
+
+
+def test_prefill_full_size_sampled_rows(O, mlxq_dev):
+    """The chunked-prefill workload at full size (Lq = 2048 queries at offset
+    30720 into a 32768-key 4-bit cache, Hq=32, Hkv=8, D=128, causal): the
+    whole launch runs on the GPU; sampled query rows are checked against the
+    oracle, where causal row i attends exactly keys [0, 30720 + i] (an
+    unmasked oracle call over that prefix)."""
+    from mlxq import ops
+
+    B, Hq, Hkv, L, N, D, gs, bits = 1, 32, 8, 2048, 32768, 128, 64, 4
+    q, kq, vq = case(O, B, Hq, Hkv, L, N, D, gs, bits, BF16, 21)
+    scale = D ** -0.5
+    got = run(O, mlxq_dev, q, kq, vq, BF16, scale, gs, bits, mask=ops.Mask("causal"))
+    assert got.shape == (B, Hq, L, D) and np.isfinite(got).all()
+    for i in (0, 1, 63, 64, 511, 1024, 2046, 2047):
+        n = N - L + i + 1
+        pre = lambda t: tuple(a[:, :, :n] for a in t)
+        ref = O.sdpa(q[:, :, i:i + 1], pre(kq), pre(vq), scale=scale, gs=gs, bits=bits, dtype=BF16)
+        assert_close(got[:, :, i:i + 1], ref, what=f"prefill row {i}", dtype=BF16)
