@@ -15,6 +15,9 @@ Also measured in the same run and reported beside it:
                         U[512, 32768] and ring offsets U[0, 4096), 4-bit
   qmv_qmm               x [M, 4096] @ W[14336, 4096]^T and x [M, 14336] @
                         W[4096, 14336]^T, 4-bit group 64, M in {1, 4, 16, 64}
+  moe_gather_decode     gather_qmm of one decode token against top-8 of 128
+                        stacked 4-bit experts: gate_up [1408, 2816] and down
+                        [2816, 704] (the 26B-A4B expert shapes)
   prefill_chunk         Lq=2048 new queries over 32768 cached keys (4-bit),
                         Hq=32 Hkv=8 D=128, causal
   cpu_baseline          the CPU oracle's decode on the host, bounded sample
@@ -220,6 +223,46 @@ def qmv_workload(M=1, N=14336, K=4096, gs=64, bits=4, seed=0, nsets=NSETS):
     return launch, algo, (sets, xs, y)
 
 
+# ------------------------------------------------------------ MoE gather
+
+def moe_gather_workload(N, K, E=128, topk=8, B=1, gs=64, bits=4, seed=60, nsets=NSETS):
+    """SwitchGLU decode over E stacked 4-bit experts [E, N, K]: x [B, 1, K]
+    against top-k indices [B, 1, k] (gather_qmm, output element i reading x
+    row i // k).  16 experts are quantized and copied into the E slots (E
+    distinct buffers, E x expert bytes > the Infinity Cache); each step takes
+    the next of nsets seeded top-k selections."""
+    from mlxq import _lib, ops
+    from mlxq.array import DeviceArray
+
+    src = ops.quantize(rand_t((16, N, K), seed, BF16, 0.02), gs, bits)
+    parts = []
+    for a in (src.packed, src.scales, src.biases):
+        full = DeviceArray.empty((E,) + a.shape[1:], a.dtype)
+        per = a.nbytes // 16
+        for e in range(E):
+            _lib.call("mlxq_memcpy_dtod", full.ptr + e * per, a.ptr + (e % 16) * per, per, None)
+        parts.append(full)
+    src.dispose()
+    wp, ws, wb = parts
+    r = np.random.default_rng(seed + 1)
+    idx = [DeviceArray.fromNumpy(np.stack([r.choice(E, topk, replace=False) for _ in range(B)]).astype(np.uint32)
+                                 .ravel(), 3) for _ in range(nsets)]
+    xmap = DeviceArray.fromNumpy(np.arange(B * topk, dtype=np.int32) // topk, 7)
+    xs = [rand_t((B, 1, K), seed + 20 + i) for i in range(nsets)]
+    y = DeviceArray.empty((B * topk, 1, N), BF16)
+    L = _lib.lib()
+
+    def launch(i):
+        rc = L.mlxq_gather_qmm(xs[i % nsets].ptr, BF16, B, B * topk, 1, K, xmap.ptr, idx[i % nsets].ptr, wp.ptr,
+                               ws.ptr, wb.ptr, E, N, gs, bits, 1, y.ptr, None)
+        if rc:
+            raise RuntimeError(L.mlxq_last_error().decode())
+
+    expert_bytes = N * K * bits // 8 + 2 * 2 * N * (K // gs)
+    algo = B * topk * expert_bytes + B * K * 2 + B * topk * N * 2
+    return launch, algo, (parts, idx, xmap, xs, y)
+
+
 # ----------------------------------------------------------------- prefill
 
 def prefill_workload(B=1, Hq=32, Hkv=8, D=128, Lq=2048, N=32768, gs=64, bits=4, seed=7):
@@ -329,6 +372,16 @@ def main():
                                         "GB/s": round(b3 / (ms3 * 1e-3) / 1e9, 1),
                                         "pct_hbm_peak": round(100 * b3 / (ms3 * 1e-3) / 1e9 / HBM_PEAK_GBS, 1)}
         del k3
+        log("bench: MoE gather_qmm decode")
+        moe = {}
+        for name, (n, k) in (("gate_up", (1408, 2816)), ("down", (2816, 704))):
+            lm, bm, km = moe_gather_workload(n, k)
+            msm = timer.graph_step_ms(lm, 100, 10)
+            moe[name] = {"N": n, "K": k, "us_per_call": round(msm * 1e3, 3), "algorithmic_bytes": bm,
+                         "GB/s": round(bm / (msm * 1e-3) / 1e9, 1),
+                         "pct_hbm_peak": round(100 * bm / (msm * 1e-3) / 1e9 / HBM_PEAK_GBS, 1)}
+            del km
+        extra["moe_gather_decode"] = moe
         log("bench: chunked prefill")
         l5, f5, k5 = prefill_workload()
         m5, md5 = timer.per_launch_us(l5, 10)

@@ -142,6 +142,28 @@ int mlxq_quantized_matmul(const void* x, int dtype, int64_t batch, int64_t M, in
                           const uint32_t* w, const void* scales, const void* biases, int64_t w_batch,
                           int64_t N, int group_size, int bits, int transpose, void* y, void* stream);
 
+/* mx.gather_qmm with rhs_indices and no lhs_indices -- replaces
+ * mlx_gather_qmm as bound by ops.gatherQmm (src/mlx/ops.ts:186-204,
+ * src/mlx/ffi.ts:167) for QuantizedSwitchLinear.forward (MoE experts,
+ * src/model/gemma4-base.ts:1615-1645).
+ * Output batch element i < batch computes y[i] = x[x_map[i]] @ W[e]^T with
+ * e = rhs_indices[i] (transpose=1; transpose=0: x[..] @ W[e]).
+ * x: [x_batch, M, K] T.  w: [n_experts, N, K*bits/32] (transpose=1) or
+ * [n_experts, K, N*bits/32], scales/biases per expert as in
+ * mlxq_quantized_matmul.  x_map: [batch] int32 on the device, the x batch
+ * element of each output element -- the broadcast of x's batch dims against
+ * rhs_indices' shape, computed by the caller (SwitchGLU's
+ * expand_dims(x, (-2, -3)) against indices [B, L, k] gives x_map[i] = i / k,
+ * src/model/gemma4.ts:434-438); NULL means x_map[i] = i (x_batch == batch).
+ * rhs_indices: [batch] uint32 on the device.  An index outside [0, x_batch)
+ * or [0, n_experts) yields a zero output row (MLX leaves it undefined).
+ * sorted_indices (a scheduling hint in MLX) has no counterpart: results do
+ * not depend on it.  y: [batch, M, N] T, fp32 accumulation. */
+int mlxq_gather_qmm(const void* x, int dtype, int64_t x_batch, int64_t batch, int64_t M, int64_t K,
+                    const int32_t* x_map, const uint32_t* rhs_indices, const uint32_t* w, const void* scales,
+                    const void* biases, int64_t n_experts, int64_t N, int group_size, int bits, int transpose,
+                    void* y, void* stream);
+
 /* ------------------------------------------------------------------ sdpa */
 
 /* quantizedSdpa(q, kq, vq, scale, mask, groupSize, bits) -- replaces the

@@ -21,13 +21,34 @@
 // without a branch) and reduce their partial rows in LDS (fixed order, no
 // cross-workgroup traffic).
 //
-// Everything else (transpose = false, 2-bit, group 32, fp32 activations,
-// larger M) takes the dequantize-to-LDS MFMA kernel or the VALU kernel below.
+// Larger M (or K too long for qmv's x slices) takes the tiled MFMA GEMM;
+// everything else (transpose = false, 2-bit, fp32 activations) the VALU
+// kernel below.  All three resolve a batch element through a BatchMap, which
+// also serves mx.gather_qmm (an x row map and an expert index per element).
 #include <cstdlib>
 
 #include "mfma_common.h"
 
 namespace {
+
+// Batch element -> (x batch element, weight matrix).  quantized_matmul:
+// xb = b, wb = b / w_rep.  gather_qmm: xb = x_map[b] (or b), wb = w_idx[b].
+// An index outside [0, x_batch) / [0, n_w) marks the element's x rows or
+// weights as absent: the kernels then read zeros (zero-sized descriptors),
+// so the output rows are zeros and no access leaves the arrays.
+struct BatchMap {
+  const int32_t* x_map;
+  const uint32_t* w_idx;
+  int64_t x_batch, n_w, w_rep;
+  __device__ __forceinline__ void resolve(int64_t b, int64_t& xb, bool& xok, int64_t& wb, bool& wok) const {
+    xb = x_map ? (int64_t)x_map[b] : b;
+    wb = w_idx ? (int64_t)w_idx[b] : b / w_rep;
+    xok = xb >= 0 && xb < x_batch;
+    wok = wb >= 0 && wb < n_w;
+    if (!xok) xb = 0;
+    if (!wok) wb = 0;
+  }
+};
 
 // weight tiles each qmv wave keeps in flight
 #ifndef QMV_WIN
@@ -38,7 +59,7 @@ template <typename T, int BITS, int GS, int MB, int R, int TPW, int MR, int XC>
 __global__ void __launch_bounds__(512) qmv_kernel(const uint16_t* __restrict__ x, int M, int K,
                                                   const uint32_t* __restrict__ w,
                                                   const uint16_t* __restrict__ scales,
-                                                  const uint16_t* __restrict__ biases, int N, int w_rep,
+                                                  const uint16_t* __restrict__ biases, int N, BatchMap bm,
                                                   uint16_t* __restrict__ y) {
   using CO = CodeOps<T, BITS>;
   constexpr int TILE_K = 512 / BITS;                 // codes per 64-byte row segment
@@ -54,14 +75,17 @@ __global__ void __launch_bounds__(512) qmv_kernel(const uint16_t* __restrict__ x
   const int tid = threadIdx.x, lane = tid & 63, nw = blockDim.x >> 6;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar offsets need it
   const int ln = lane & 15, lq = lane >> 4;
-  const int bidx = blockIdx.y, wb = bidx / w_rep;
+  const int bidx = blockIdx.y;
+  int64_t xb, wb;
+  bool xok, wok;
+  bm.resolve(bidx, xb, xok, wb, wok);
   const int n0 = blockIdx.x * 16 * R;
-  const int rows = min(16 * R, N - n0);
+  const int rows = wok ? min(16 * R, N - n0) : 0;
   const int G = K / GS, KT = K / TILE_K;
   const uint32_t row_bytes = (uint32_t)K * BITS / 8;
-  x += (int64_t)bidx * M * K;
+  x += xb * M * K;
   y += (int64_t)bidx * M * N;
-  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (uint32_t)(M * K * 2));
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, xok ? (uint32_t)(M * K * 2) : 0u);
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(w + ((int64_t)wb * N + n0) * (row_bytes / 4), (uint32_t)rows * row_bytes);
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(scales + ((int64_t)wb * N + n0) * G, (uint32_t)(rows * G * 2));
   const __amdgpu_buffer_rsrc_t rb = make_rsrc(biases + ((int64_t)wb * N + n0) * G, (uint32_t)(rows * G * 2));
@@ -276,7 +300,7 @@ template <typename T, int BITS, int GS, int BM, int BN>
 __global__ void __launch_bounds__(256) qmm_tile_kernel(const uint16_t* __restrict__ x, int M, int K,
                                                        const uint32_t* __restrict__ w,
                                                        const uint16_t* __restrict__ scales,
-                                                       const uint16_t* __restrict__ biases, int N, int w_rep,
+                                                       const uint16_t* __restrict__ biases, int N, BatchMap bm,
                                                        int KS, int KTS, uint32_t sb_bytes,
                                                        uint16_t* __restrict__ y, float* __restrict__ part) {
   using SH = TileShape<BM, BN>;
@@ -302,18 +326,21 @@ __global__ void __launch_bounds__(256) qmm_tile_kernel(const uint16_t* __restric
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / SH::WGN, wn = wave % SH::WGN;
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-  const int bidx = blockIdx.z / KS, split = blockIdx.z % KS, wb = bidx / w_rep;
+  const int bidx = blockIdx.z / KS, split = blockIdx.z % KS;
+  int64_t xb, wb;
+  bool xok, wok;
+  bm.resolve(bidx, xb, xok, wb, wok);
   const int G = K / GS, KT = K / BK;
   const int kb = split * KTS, ke = min(KT, kb + KTS);
   const uint32_t row_bytes = (uint32_t)K * BITS / 8;
-  const int mrows = min(BM, M - m0), nrows = min(BN, N - n0);
-  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + ((int64_t)bidx * M + m0) * K, (uint32_t)(mrows * K * 2));
+  const int mrows = xok ? min(BM, M - m0) : 0, nrows = wok ? min(BN, N - n0) : 0;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + (xb * M + m0) * K, (uint32_t)(mrows * K * 2));
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(w + ((int64_t)wb * N + n0) * (row_bytes / 4), (uint32_t)nrows * row_bytes);
   // scales / biases: whole arrays (4-byte aligned), read as the dword that
   // holds the wanted 16-bit value (a 16-bit load feeding the prefetch ring
   // would be widened, and so waited for, right at the load)
-  const __amdgpu_buffer_rsrc_t rs = make_rsrc(scales, sb_bytes);
-  const __amdgpu_buffer_rsrc_t rb = make_rsrc(biases, sb_bytes);
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(scales, wok ? sb_bytes : 0u);
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(biases, wok ? sb_bytes : 0u);
   const int64_t sb_elem0 = ((int64_t)wb * N + n0) * G;  // tile's first (row, group) element
   constexpr uint32_t OOB = 0x80000000u;  // past every descriptor: reads 0
 
@@ -535,8 +562,6 @@ __global__ void __launch_bounds__(256) qmm_splitk_reduce_kernel(const float4* __
 // (x staging amortised over 128 weight rows), 128 x 128 once those give every
 // CU a workgroup, else 64 x 64; K is split (fp32 partials + reduce) until every CU
 // has a workgroup, keeping at least 8 K-steps per split.
-inline int64_t w_batch_of(int64_t batch, int64_t w_rep) { return batch / w_rep; }
-
 // MLXQ_QMM_KS: fixed K split (power of two) for the tiled GEMM (tuning)
 int qmm_ks_override() {
   static const int v = [] {
@@ -548,7 +573,7 @@ int qmm_ks_override() {
 
 template <typename T, int BITS, int GS, int BM, int BN>
 int launch_qmm_tile_inst(const void* x, int64_t batch, int64_t M, int64_t K, const uint32_t* w, const void* scales,
-                         const void* biases, int64_t w_rep, int64_t N, void* y, hipStream_t s) {
+                         const void* biases, const BatchMap& bm, int64_t N, void* y, hipStream_t s) {
   const int64_t tiles = ((N + BN - 1) / BN) * ((M + BM - 1) / BM) * batch;
   const int64_t KT = K / 64;
   const int64_t target = mlxq::device_cu_count();
@@ -572,8 +597,8 @@ int launch_qmm_tile_inst(const void* x, int64_t batch, int64_t M, int64_t K, con
   MLXQ_CHECK(batch * KS < 65536, "qmm: batch too large for one launch");
   dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM), (unsigned)(batch * KS));
   hipLaunchKernelGGL((qmm_tile_kernel<T, BITS, GS, BM, BN>), grid, dim3(256), 0, s, (const uint16_t*)x, (int)M,
-                     (int)K, w, (const uint16_t*)scales, (const uint16_t*)biases, (int)N, (int)w_rep, KS, KTS,
-                     (uint32_t)(((w_batch_of(batch, w_rep) * N * (K / GS)) * 2 + 3) & ~(int64_t)3), (uint16_t*)y, part);
+                     (int)K, w, (const uint16_t*)scales, (const uint16_t*)biases, (int)N, bm, KS, KTS,
+                     (uint32_t)(((bm.n_w * N * (K / GS)) * 2 + 3) & ~(int64_t)3), (uint16_t*)y, part);
   MLXQ_LAUNCHED("qmm_tile_kernel");
   if (KS > 1) {
     const int64_t n4 = batch * M * N / 4;
@@ -586,14 +611,14 @@ int launch_qmm_tile_inst(const void* x, int64_t batch, int64_t M, int64_t K, con
 
 template <typename T, int BITS, int GS>
 int launch_qmm_tile(const void* x, int64_t batch, int64_t M, int64_t K, const uint32_t* w, const void* scales,
-                    const void* biases, int64_t w_rep, int64_t N, void* y, hipStream_t s) {
+                    const void* biases, const BatchMap& bm, int64_t N, void* y, hipStream_t s) {
   if (M <= 32)
-    return launch_qmm_tile_inst<T, BITS, GS, 32, 128>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);
+    return launch_qmm_tile_inst<T, BITS, GS, 32, 128>(x, batch, M, K, w, scales, biases, bm, N, y, s);
   if (M >= 128 && ((N + 127) / 128) * ((M + 127) / 128) * batch >= mlxq::device_cu_count())
-    return launch_qmm_tile_inst<T, BITS, GS, 128, 128>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);
+    return launch_qmm_tile_inst<T, BITS, GS, 128, 128>(x, batch, M, K, w, scales, biases, bm, N, y, s);
   if (M <= 64)
-    return launch_qmm_tile_inst<T, BITS, GS, 64, 128>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);
-  return launch_qmm_tile_inst<T, BITS, GS, 64, 64>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);
+    return launch_qmm_tile_inst<T, BITS, GS, 64, 128>(x, batch, M, K, w, scales, biases, bm, N, y, s);
+  return launch_qmm_tile_inst<T, BITS, GS, 64, 64>(x, batch, M, K, w, scales, biases, bm, N, y, s);
 }
 
 // ---- generic VALU path -----------------------------------------------------
@@ -604,19 +629,25 @@ template <typename T, int BITS>
 __global__ void __launch_bounds__(256) qmm_generic_kernel(const void* __restrict__ xv, int64_t M, int64_t K,
                                                            const uint32_t* __restrict__ w, const void* __restrict__ sv,
                                                            const void* __restrict__ bv, int64_t N, int gs,
-                                                           int transpose, int64_t w_rep, void* __restrict__ yv) {
+                                                           int transpose, BatchMap bm, void* __restrict__ yv) {
   using S = typename T::storage;
   const S* x = reinterpret_cast<const S*>(xv);
   const S* scales = reinterpret_cast<const S*>(sv);
   const S* biases = reinterpret_cast<const S*>(bv);
   S* y = reinterpret_cast<S*>(yv);
   const int64_t bidx = blockIdx.z;
-  const int64_t wb = bidx / w_rep;
+  int64_t xb, wb;
+  bool xok, wok;
+  bm.resolve(bidx, xb, xok, wb, wok);
   const int64_t mn = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (mn >= M * N) return;
   const int64_t m = mn / N, n = mn % N;
-  x += bidx * M * K;
+  x += xb * M * K;
   y += bidx * M * N;
+  if (!xok || !wok) {  // absent x rows or weights: zeros
+    Conv<T>::store(y, m * N + n, 0.f);
+    return;
+  }
   constexpr uint32_t MASK = (1u << BITS) - 1u;
   constexpr int E = 32 / BITS;
   float acc = 0.f;
@@ -693,7 +724,7 @@ bool plan_qmv(int bits, int gs, int64_t M, int64_t K, int64_t N, int64_t batch, 
 
 template <typename T, int BITS, int GS, int MB, int R, int TPW, int MR, int XC>
 int launch_qmv_inst(const void* x, int64_t batch, int64_t M, int64_t K, const uint32_t* w, const void* scales,
-                    const void* biases, int64_t w_rep, int64_t N, void* y, const QmvPlan& p, hipStream_t s) {
+                    const void* biases, const BatchMap& bm, int64_t N, void* y, const QmvPlan& p, hipStream_t s) {
   if constexpr (TPW * (512 / BITS) / GS % 4 != 0) {
     return mlxq::fail(MLXQ_ERR_UNSUPPORTED, "qmv: tile geometry");
   } else {
@@ -707,7 +738,7 @@ int launch_qmv_inst(const void* x, int64_t batch, int64_t M, int64_t K, const ui
     }
     dim3 grid((unsigned)((N + 16 * R - 1) / (16 * R)), (unsigned)batch);
     hipLaunchKernelGGL(kern, grid, dim3(p.NW * 64), p.lds, s, (const uint16_t*)x, (int)M, (int)K, w,
-                       (const uint16_t*)scales, (const uint16_t*)biases, (int)N, (int)w_rep, (uint16_t*)y);
+                       (const uint16_t*)scales, (const uint16_t*)biases, (int)N, bm, (uint16_t*)y);
     MLXQ_LAUNCHED("qmv_kernel");
     return MLXQ_OK;
   }
@@ -715,10 +746,10 @@ int launch_qmv_inst(const void* x, int64_t batch, int64_t M, int64_t K, const ui
 
 template <typename T, int BITS, int GS>
 int launch_qmv(const void* x, int64_t batch, int64_t M, int64_t K, const uint32_t* w, const void* scales,
-               const void* biases, int64_t w_rep, int64_t N, void* y, const QmvPlan& p, hipStream_t s) {
+               const void* biases, const BatchMap& bm, int64_t N, void* y, const QmvPlan& p, hipStream_t s) {
 #define QMV_I(MBV, RV, TV, MRV, XCV)                                                                            \
   if (p.MB == MBV && p.R == RV && p.TPW == TV && p.MR == MRV && p.XC == XCV)                                    \
-    return launch_qmv_inst<T, BITS, GS, MBV, RV, TV, MRV, XCV>(x, batch, M, K, w, scales, biases, w_rep, N, y, p, s);
+    return launch_qmv_inst<T, BITS, GS, MBV, RV, TV, MRV, XCV>(x, batch, M, K, w, scales, biases, bm, N, y, p, s);
   QMV_I(1, 1, 4, 2, 8) QMV_I(1, 1, 8, 2, 8) QMV_I(1, 1, 16, 2, 8) QMV_I(1, 2, 4, 2, 8) QMV_I(1, 2, 8, 2, 8)
   QMV_I(1, 2, 16, 2, 8) QMV_I(1, 1, 4, 4, 8) QMV_I(1, 1, 8, 4, 8) QMV_I(1, 1, 16, 4, 8) QMV_I(1, 2, 4, 4, 8)
   QMV_I(1, 2, 8, 4, 8) QMV_I(1, 2, 16, 4, 8) QMV_I(2, 1, 4, 4, 8) QMV_I(2, 1, 8, 4, 8) QMV_I(2, 1, 16, 4, 8)
@@ -730,59 +761,45 @@ int launch_qmv(const void* x, int64_t batch, int64_t M, int64_t K, const uint32_
   return mlxq::fail(MLXQ_ERR_UNSUPPORTED, "qmv: no instance for this plan");
 }
 
-}  // namespace
-
-extern "C" int mlxq_quantized_matmul(const void* x, int dtype, int64_t batch, int64_t M, int64_t K,
-                                     const uint32_t* w, const void* scales, const void* biases, int64_t w_batch,
-                                     int64_t N, int group_size, int bits, int transpose, void* y, void* stream) {
-  MLXQ_REQUIRE_INIT();
-  MLXQ_CHECK(mlxq::dtype_supported(dtype), "dtype must be float16, bfloat16 or float32");
-  MLXQ_CHECK(bits == 2 || bits == 4 || bits == 8, "bits must be 2, 4 or 8");
-  MLXQ_CHECK(group_size == 32 || group_size == 64 || group_size == 128, "group_size must be 32, 64 or 128");
-  MLXQ_CHECK(batch >= 0 && M >= 0 && K >= 0 && N >= 0, "negative extent");
-  MLXQ_CHECK(w_batch >= 1 && batch % w_batch == 0, "batch must be a multiple of w_batch");
-  const int64_t grouped = transpose ? K : N;
-  MLXQ_CHECK(grouped % group_size == 0, "the quantized axis must be a multiple of group_size");
-  if (batch == 0 || M == 0 || N == 0) return MLXQ_OK;
-  MLXQ_CHECK(x && w && scales && biases && y, "null buffer");
-  hipStream_t s = mlxq::resolve_stream(stream);
-  const int64_t w_rep = batch / w_batch;
-  if (K == 0) return mlxq_fill_zero(y, (uint64_t)(batch * M * N * mlxq::dtype_bytes(dtype)), stream);
-
+// Kernel choice shared by quantized_matmul and gather_qmm: qmv for small M,
+// the tiled MFMA GEMM for larger M, the VALU kernel for everything else.
+int qmm_dispatch(const void* x, int dtype, int64_t batch, int64_t M, int64_t K, const uint32_t* w,
+                 const void* scales, const void* biases, const BatchMap& bm, int64_t N, int group_size, int bits,
+                 int transpose, void* y, hipStream_t s) {
   QmvPlan plan;
   const bool qmv_ok = transpose && mlxq::is_half_dtype(dtype) && (bits == 4 || bits == 8) &&
                       (group_size == 64 || group_size == 128) && (uintptr_t)x % 16 == 0 &&
                       (uintptr_t)w % 16 == 0 && (uintptr_t)scales % 8 == 0 && (uintptr_t)biases % 8 == 0 &&
-                      K * M < ((int64_t)1 << 30) &&
+                      K * M < ((int64_t)1 << 30) && batch < 65536 &&
                       plan_qmv(bits, group_size, M, K, N, batch, &plan);
   if (qmv_ok) {
     if (dtype == MLXQ_BFLOAT16) {
       if (bits == 4)
-        return group_size == 64 ? launch_qmv<BF16, 4, 64>(x, batch, M, K, w, scales, biases, w_rep, N, y, plan, s)
-                                : launch_qmv<BF16, 4, 128>(x, batch, M, K, w, scales, biases, w_rep, N, y, plan, s);
-      return group_size == 64 ? launch_qmv<BF16, 8, 64>(x, batch, M, K, w, scales, biases, w_rep, N, y, plan, s)
-                              : launch_qmv<BF16, 8, 128>(x, batch, M, K, w, scales, biases, w_rep, N, y, plan, s);
+        return group_size == 64 ? launch_qmv<BF16, 4, 64>(x, batch, M, K, w, scales, biases, bm, N, y, plan, s)
+                                : launch_qmv<BF16, 4, 128>(x, batch, M, K, w, scales, biases, bm, N, y, plan, s);
+      return group_size == 64 ? launch_qmv<BF16, 8, 64>(x, batch, M, K, w, scales, biases, bm, N, y, plan, s)
+                              : launch_qmv<BF16, 8, 128>(x, batch, M, K, w, scales, biases, bm, N, y, plan, s);
     }
     if (bits == 4)
-      return group_size == 64 ? launch_qmv<F16, 4, 64>(x, batch, M, K, w, scales, biases, w_rep, N, y, plan, s)
-                              : launch_qmv<F16, 4, 128>(x, batch, M, K, w, scales, biases, w_rep, N, y, plan, s);
-    return group_size == 64 ? launch_qmv<F16, 8, 64>(x, batch, M, K, w, scales, biases, w_rep, N, y, plan, s)
-                            : launch_qmv<F16, 8, 128>(x, batch, M, K, w, scales, biases, w_rep, N, y, plan, s);
+      return group_size == 64 ? launch_qmv<F16, 4, 64>(x, batch, M, K, w, scales, biases, bm, N, y, plan, s)
+                              : launch_qmv<F16, 4, 128>(x, batch, M, K, w, scales, biases, bm, N, y, plan, s);
+    return group_size == 64 ? launch_qmv<F16, 8, 64>(x, batch, M, K, w, scales, biases, bm, N, y, plan, s)
+                            : launch_qmv<F16, 8, 128>(x, batch, M, K, w, scales, biases, bm, N, y, plan, s);
   }
 
   const bool tile_ok = transpose && mlxq::is_half_dtype(dtype) && (bits == 4 || bits == 8) && K % 64 == 0 &&
-                      (uintptr_t)x % 16 == 0 && (uintptr_t)w % 16 == 0 && (uintptr_t)scales % 4 == 0 &&
-                      (uintptr_t)biases % 4 == 0 && M * K * 2 < ((int64_t)1 << 31) && N * K < ((int64_t)1 << 31) &&
-                      w_batch * N * (K / group_size) * 2 < ((int64_t)1 << 31);
+                       (uintptr_t)x % 16 == 0 && (uintptr_t)w % 16 == 0 && (uintptr_t)scales % 4 == 0 &&
+                       (uintptr_t)biases % 4 == 0 && M * K * 2 < ((int64_t)1 << 31) &&
+                       N * K < ((int64_t)1 << 31) && bm.n_w * N * (K / group_size) * 2 < ((int64_t)1 << 31);
   if (tile_ok) {
 #define QMM_TILE_T(TT)                                                                                           \
   switch (bits * 1000 + group_size) {                                                                           \
-    case 4032: return launch_qmm_tile<TT, 4, 32>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);            \
-    case 4064: return launch_qmm_tile<TT, 4, 64>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);            \
-    case 4128: return launch_qmm_tile<TT, 4, 128>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);           \
-    case 8032: return launch_qmm_tile<TT, 8, 32>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);            \
-    case 8064: return launch_qmm_tile<TT, 8, 64>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);            \
-    default: return launch_qmm_tile<TT, 8, 128>(x, batch, M, K, w, scales, biases, w_rep, N, y, s);             \
+    case 4032: return launch_qmm_tile<TT, 4, 32>(x, batch, M, K, w, scales, biases, bm, N, y, s);               \
+    case 4064: return launch_qmm_tile<TT, 4, 64>(x, batch, M, K, w, scales, biases, bm, N, y, s);               \
+    case 4128: return launch_qmm_tile<TT, 4, 128>(x, batch, M, K, w, scales, biases, bm, N, y, s);              \
+    case 8032: return launch_qmm_tile<TT, 8, 32>(x, batch, M, K, w, scales, biases, bm, N, y, s);               \
+    case 8064: return launch_qmm_tile<TT, 8, 64>(x, batch, M, K, w, scales, biases, bm, N, y, s);               \
+    default: return launch_qmm_tile<TT, 8, 128>(x, batch, M, K, w, scales, biases, bm, N, y, s);                \
   }
     if (dtype == MLXQ_BFLOAT16) {
       QMM_TILE_T(BF16)
@@ -794,23 +811,63 @@ extern "C" int mlxq_quantized_matmul(const void* x, int dtype, int64_t batch, in
 
   const int64_t outs = M * N;
   MLXQ_CHECK(outs <= (int64_t)0x7fffffff * 256, "output too large");
+  MLXQ_CHECK(batch < 65536, "batch too large for one launch");
   dim3 grid((unsigned)((outs + 255) / 256), 1, (unsigned)batch);
   MLXQ_DISPATCH_T(dtype, TT, {
     switch (bits) {
       case 2:
         hipLaunchKernelGGL((qmm_generic_kernel<TT, 2>), grid, dim3(256), 0, s, x, M, K, w, scales, biases, N,
-                           group_size, transpose, w_rep, y);
+                           group_size, transpose, bm, y);
         break;
       case 4:
         hipLaunchKernelGGL((qmm_generic_kernel<TT, 4>), grid, dim3(256), 0, s, x, M, K, w, scales, biases, N,
-                           group_size, transpose, w_rep, y);
+                           group_size, transpose, bm, y);
         break;
       default:
         hipLaunchKernelGGL((qmm_generic_kernel<TT, 8>), grid, dim3(256), 0, s, x, M, K, w, scales, biases, N,
-                           group_size, transpose, w_rep, y);
+                           group_size, transpose, bm, y);
         break;
     }
   });
   MLXQ_LAUNCHED("qmm_generic_kernel");
   return MLXQ_OK;
+}
+
+}  // namespace
+
+// Argument checks both entry points share.
+#define QMM_COMMON_CHECKS()                                                                                  \
+  MLXQ_REQUIRE_INIT();                                                                                       \
+  MLXQ_CHECK(mlxq::dtype_supported(dtype), "dtype must be float16, bfloat16 or float32");                    \
+  MLXQ_CHECK(bits == 2 || bits == 4 || bits == 8, "bits must be 2, 4 or 8");                                 \
+  MLXQ_CHECK(group_size == 32 || group_size == 64 || group_size == 128, "group_size must be 32, 64 or 128"); \
+  MLXQ_CHECK(batch >= 0 && M >= 0 && K >= 0 && N >= 0, "negative extent");                                   \
+  MLXQ_CHECK((transpose ? K : N) % group_size == 0, "the quantized axis must be a multiple of group_size")
+
+extern "C" int mlxq_quantized_matmul(const void* x, int dtype, int64_t batch, int64_t M, int64_t K,
+                                     const uint32_t* w, const void* scales, const void* biases, int64_t w_batch,
+                                     int64_t N, int group_size, int bits, int transpose, void* y, void* stream) {
+  QMM_COMMON_CHECKS();
+  MLXQ_CHECK(w_batch >= 1 && batch % w_batch == 0, "batch must be a multiple of w_batch");
+  if (batch == 0 || M == 0 || N == 0) return MLXQ_OK;
+  MLXQ_CHECK(x && w && scales && biases && y, "null buffer");
+  hipStream_t s = mlxq::resolve_stream(stream);
+  if (K == 0) return mlxq_fill_zero(y, (uint64_t)(batch * M * N * mlxq::dtype_bytes(dtype)), stream);
+  const BatchMap bm{nullptr, nullptr, batch, w_batch, batch / w_batch};
+  return qmm_dispatch(x, dtype, batch, M, K, w, scales, biases, bm, N, group_size, bits, transpose, y, s);
+}
+
+extern "C" int mlxq_gather_qmm(const void* x, int dtype, int64_t x_batch, int64_t batch, int64_t M, int64_t K,
+                               const int32_t* x_map, const uint32_t* rhs_indices, const uint32_t* w,
+                               const void* scales, const void* biases, int64_t n_experts, int64_t N,
+                               int group_size, int bits, int transpose, void* y, void* stream) {
+  QMM_COMMON_CHECKS();
+  MLXQ_CHECK(x_batch >= 0 && n_experts >= 1, "x_batch must be >= 0 and n_experts >= 1");
+  MLXQ_CHECK(x_map || x_batch == batch, "without x_map, x_batch must equal batch");
+  if (batch == 0 || M == 0 || N == 0) return MLXQ_OK;
+  MLXQ_CHECK(x && w && scales && biases && y && rhs_indices, "null buffer");
+  hipStream_t s = mlxq::resolve_stream(stream);
+  if (K == 0) return mlxq_fill_zero(y, (uint64_t)(batch * M * N * mlxq::dtype_bytes(dtype)), stream);
+  const BatchMap bm{x_map, rhs_indices, x_batch, n_experts, 1};
+  return qmm_dispatch(x, dtype, batch, M, K, w, scales, biases, bm, N, group_size, bits, transpose, y, s);
 }

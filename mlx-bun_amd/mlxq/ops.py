@@ -2,7 +2,7 @@
 
 Names, argument meaning and error behaviour follow src/mlx/ops.ts
 (quantize :615-641, dequantize :212-225, quantizedMatmul :171-184,
-quantizedMatmulQT :760-775) and src/model/gemma4-base.ts (Mask :21-32,
+gatherQmm :186-204, quantizedMatmulQT :760-775) and src/model/gemma4-base.ts (Mask :21-32,
 quantizedSdpa :1560-1578, createCausalMask :1595-1615).  Every op runs
 asynchronously on the library's default stream; reading a result back
 (toFloat32/rawNumpy) synchronises.
@@ -119,6 +119,77 @@ def quantizedMatmulQT(x: DeviceArray, qt: QuantizedTensor, transpose: bool, grou
                       bits: int) -> DeviceArray:
     """quantized_matmul against a QuantizedTensor (x @ qt^T or x @ qt)."""
     return quantizedMatmul(x, qt.packed, qt.scales, qt.biases, QuantSpec(bits, groupSize), transpose)
+
+
+def gather_batch_maps(x_lead, idx_shape):
+    """Broadcast x's leading dims against rhs_indices' shape, as gather_qmm
+    broadcasts its batch dims: returns (out_lead, x_map), x_map[i] being the x
+    batch element output element i reads, or None when that is i itself."""
+    x_lead, idx_shape = tuple(x_lead), tuple(idx_shape)
+    out_lead = tuple(np.broadcast_shapes(x_lead, idx_shape))
+    if x_lead == out_lead:
+        return out_lead, None
+    x_batch = int(np.prod(x_lead)) if x_lead else 1
+    xm = np.broadcast_to(np.arange(x_batch, dtype=np.int32).reshape(x_lead), out_lead).ravel()
+    return out_lead, np.ascontiguousarray(xm)
+
+
+def gatherQmm(x: DeviceArray, w: DeviceArray, scales: DeviceArray, biases: Optional[DeviceArray],
+              rhsIndices: DeviceArray, spec: QuantSpec, sortedIndices: bool, transpose: bool = True) -> DeviceArray:
+    """mx.gather_qmm with rhs_indices (src/mlx/ops.ts:186-204), as
+    QuantizedSwitchLinear.forward calls it (src/model/gemma4-base.ts:1642).
+    x [..., M, K]; w [E, N, K*bits/32] (transpose) or [E, K, N*bits/32];
+    rhsIndices (uint32 or int32) selects the expert per output batch element,
+    its shape broadcasting with x's leading dims.  Returns
+    broadcast(x[..., :-2], rhsIndices) + [M, N] in x's dtype.  sortedIndices
+    is MLX's scheduling hint; results do not depend on it."""
+    _check_mode(spec.mode)
+    del sortedIndices
+    if biases is None:
+        raise ValueError("affine gather_qmm requires biases")
+    for a, n in ((x, "x"), (w, "w"), (scales, "scales"), (biases, "biases"), (rhsIndices, "rhsIndices")):
+        _need_contiguous(a, n)
+    if x.dtype != scales.dtype:
+        raise ValueError("x and scales must share a dtype")
+    if rhsIndices.dtype not in (3, 7):
+        raise ValueError("rhsIndices must be uint32 or int32")
+    if len(w.shape) != 3:
+        raise ValueError("gather_qmm: w must be [experts, rows, packed]")
+    if len(x.shape) < 2:
+        raise ValueError("gather_qmm: x must be [..., M, K]")
+    K, M = x.shape[-1], x.shape[-2]
+    E = w.shape[0]
+    if transpose:
+        N = w.shape[1]
+        if w.shape[2] * 32 // spec.bits != K:
+            raise ValueError(f"gather_qmm: x has K={K}, w holds {w.shape[2] * 32 // spec.bits}")
+    else:
+        N = w.shape[2] * 32 // spec.bits
+        if w.shape[1] != K:
+            raise ValueError(f"gather_qmm: x has K={K}, w has {w.shape[1]} rows")
+    x_lead = tuple(x.shape[:-2])
+    idx_shape = tuple(rhsIndices.shape)
+    out_lead, xm = gather_batch_maps(x_lead, idx_shape)
+    x_batch = int(np.prod(x_lead)) if x_lead else 1
+    batch = int(np.prod(out_lead)) if out_lead else 1
+    keep = []
+    x_map = None
+    if xm is not None:
+        x_map = DeviceArray.fromNumpy(xm, 7)
+        keep.append(x_map)
+    idx = rhsIndices
+    if idx_shape != out_lead:
+        host = np.broadcast_to(rhsIndices.rawNumpy().reshape(idx_shape), out_lead).ravel()
+        idx = DeviceArray.fromNumpy(np.ascontiguousarray(host), rhsIndices.dtype)
+        keep.append(idx)
+    y = DeviceArray.empty(out_lead + (M, N), x.dtype)
+    _lib.call("mlxq_gather_qmm", x.ptr, x.dtype, x_batch, batch, M, K, x_map.ptr if x_map is not None else None,
+              idx.ptr, w.ptr, scales.ptr, biases.ptr, E, N, spec.groupSize, spec.bits, int(bool(transpose)), y.ptr,
+              None)
+    # the temporaries are freed (hipFree, which waits for the device) only
+    # after the launch that reads them
+    del keep
+    return y
 
 
 # ------------------------------------------------------------------ masks

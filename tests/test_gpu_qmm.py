@@ -125,3 +125,101 @@ def test_qmm_tile(O, mlxq_dev, dtype, bits, gs, lead, M, N, K):
     x = rng_t(O, lead + (M, K), 12, dtype)
     y = run_qmm(O, mlxq_dev, x, wq, gs, bits, dtype)
     assert_close(y, x.astype(np.float64) @ deq64(O, *wq, gs, bits, dtype).T, what="tile", dtype=dtype)
+
+
+# ---------------------------------------------------------------- gather_qmm
+
+def _gather_ref(O, x, wq, idx_flat, x_map, gs, bits, dtype):
+    """float64 per-expert reference: out[i] = x[x_map[i]] @ deq(W[idx[i]])^T."""
+    p, s, b = wq
+    M, K = x.shape[-2], x.shape[-1]
+    xf = x.reshape(-1, M, K).astype(np.float64)
+    out = []
+    for i, e in enumerate(idx_flat):
+        wd = deq64(O, p[e], s[e], b[e], gs, bits, dtype)
+        out.append(xf[x_map[i]] @ wd.T)
+    return np.stack(out)
+
+
+def _gather(O, x, wq, idx, gs, bits, dtype, idx_dtype=3):
+    from mlxq import ops
+    from mlxq.array import DeviceArray
+
+    p, s, b = wq
+    y = ops.gatherQmm(DeviceArray.fromFloat32(x, x.shape, dtype), DeviceArray.fromNumpy(p, 3),
+                      DeviceArray.fromNumpy(s, dtype), DeviceArray.fromNumpy(b, dtype),
+                      DeviceArray.fromNumpy(np.asarray(idx, np.uint32 if idx_dtype == 3 else np.int32), idx_dtype),
+                      ops.QuantSpec(bits, gs), False)
+    return y.toFloat32()
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_gather_qmm_reference_case(O, mlxq_dev, bits):
+    """tests/moe-ops.test.ts: 4 experts [16, 64] group 32 on the reference's LCG
+    data (fp32), x [1, 2, 64] -> [1, 2, 1, 1, 64], indices [[2, 0], [1, 3]]:
+    gather_qmm equals a per-expert quantized_matmul loop to < 1e-5 and the
+    float64 oracle to the matmul bar."""
+    from mlxq import ops
+    from mlxq.array import DeviceArray
+
+    E, OUT, IN, GS = 4, 16, 64, 32
+    w = O.lcg_floats(E * OUT * IN, 7).reshape(E, OUT, IN)
+    wq = O.quantize(w, GS, bits, F32)
+    x = O.lcg_floats(2 * IN, 11).reshape(1, 2, IN)
+    h = x.reshape(1, 2, 1, 1, IN)
+    idx = np.array([2, 0, 1, 3], np.uint32).reshape(1, 2, 2)
+    got = _gather(O, h, wq, idx, GS, bits, F32)
+    assert got.shape == (1, 2, 2, 1, OUT)
+    p, s, b = wq
+    loop = np.zeros((2, 2, OUT), np.float32)
+    for t in range(2):
+        for j in range(2):
+            e = int(idx[0, t, j])
+            y = ops.quantizedMatmul(DeviceArray.fromFloat32(x[0, t:t + 1], (1, IN), F32), DeviceArray.fromNumpy(p[e], 3),
+                                    DeviceArray.fromNumpy(s[e], F32), DeviceArray.fromNumpy(b[e], F32),
+                                    ops.QuantSpec(bits, GS), True)
+            loop[t, j] = y.toFloat32()[0]
+    assert np.abs(got.reshape(2, 2, OUT) - loop).max() < 1e-5
+    ref = _gather_ref(O, h, wq, idx.ravel(), [0, 0, 1, 1], GS, bits, F32)
+    assert_close(got.reshape(4, 1, OUT), ref, what="gather ref case", dtype=F32)
+
+
+@pytest.fixture(scope="module")
+def experts_up(O):
+    """16 experts of the 26B-A4B gate_up shape [1408, 2816], 4-bit group 64
+    (docs/design/diffusion-gemma-port.md:357; 16 of the 128 experts)."""
+    w = rng_t(O, (16, 1408, 2816), 31, BF16, 0.02)
+    return O.quantize(w, 64, 4, BF16)
+
+
+@pytest.mark.parametrize("B", [1, 4])
+def test_gather_qmm_moe_decode(O, mlxq_dev, experts_up, B):
+    """SwitchGLU decode: x [B, 1, H] -> [B, 1, 1, 1, H] against top-8 indices
+    [B, 1, 8] (qmv per (token, expert) through the row map)."""
+    r = np.random.default_rng(40 + B)
+    idx = np.stack([r.choice(16, 8, replace=False) for _ in range(B)]).astype(np.uint32).reshape(B, 1, 8)
+    x = rng_t(O, (B, 1, 1, 1, 2816), 41 + B, BF16)
+    got = _gather(O, x, experts_up, idx, 64, 4, BF16)
+    assert got.shape == (B, 1, 8, 1, 1408)
+    ref = _gather_ref(O, x, experts_up, idx.ravel(), [i // 8 for i in range(8 * B)], 64, 4, BF16)
+    assert_close(got.reshape(8 * B, 1, 1408), ref, what=f"moe decode B={B}", dtype=BF16)
+
+
+def test_gather_qmm_sorted_rows_and_bad_index(O, mlxq_dev, experts_up):
+    """The sorted path (x [rows, 1, H], indices [rows] grouped by expert) and
+    an expert index past the end (its row is zeros), int32 indices."""
+    idx = np.array([0, 0, 3, 3, 3, 9, 15, 99], np.int32)
+    x = rng_t(O, (8, 1, 2816), 50, BF16)
+    got = _gather(O, x, experts_up, idx, 64, 4, BF16, idx_dtype=7)
+    assert not got[7].any()
+    ref = _gather_ref(O, x[:7], experts_up, idx[:7], list(range(7)), 64, 4, BF16)
+    assert_close(got[:7], ref, what="sorted", dtype=BF16)
+
+
+def test_gather_qmm_many_rows_per_expert(O, mlxq_dev, experts_up):
+    """M = 40 rows per gathered matmul (the tiled GEMM through the batch map)."""
+    idx = np.array([5, 2], np.uint32)
+    x = rng_t(O, (2, 40, 2816), 51, BF16)
+    got = _gather(O, x, experts_up, idx, 64, 4, BF16)
+    ref = _gather_ref(O, x, experts_up, idx, [0, 1], 64, 4, BF16)
+    assert_close(got, ref, what="tile gather", dtype=BF16)

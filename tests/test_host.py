@@ -53,3 +53,21 @@ def test_cache_make_mask_rules():
     r.offset = 30
     m = r.makeMask(4, None)  # offset clamps to maxSize - 1 = 15; 15 + 4 > 16
     assert m.mode == "array" and m.window == 16 and m.arr.shape == (4, 19)
+
+
+def test_gather_batch_maps():
+    """gather_qmm's batch broadcast (x's leading dims against rhs_indices):
+    SwitchGLU's expand_dims(x, (-2, -3)) against indices [B, L, k] makes
+    output element (b, l, j) read x row (b, l) (src/model/gemma4.ts:434-438)."""
+    from mlxq.ops import gather_batch_maps
+
+    out, xm = gather_batch_maps((1, 2, 1), (1, 2, 2))  # tests/moe-ops.test.ts shapes
+    assert out == (1, 2, 2) and xm.tolist() == [0, 0, 1, 1]
+    out, xm = gather_batch_maps((4, 1, 1), (4, 1, 8))
+    assert out == (4, 1, 8) and xm.tolist() == [i // 8 for i in range(32)]
+    out, xm = gather_batch_maps((6,), (6,))  # sorted path: one x row per index
+    assert out == (6,) and xm is None
+    out, xm = gather_batch_maps((), (5,))  # one x broadcast to every index
+    assert out == (5,) and xm.tolist() == [0] * 5
+    out, xm = gather_batch_maps((3, 1), (1, 2))  # both sides broadcast
+    assert out == (3, 2) and xm.tolist() == [0, 0, 1, 1, 2, 2]
