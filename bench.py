@@ -18,6 +18,8 @@ Also measured in the same run and reported beside it:
   moe_gather_decode     gather_qmm of one decode token against top-8 of 128
                         stacked 4-bit experts: gate_up [1408, 2816] and down
                         [2816, 704] (the 26B-A4B expert shapes)
+  tied_head_qmv         x [1, 2816] @ W[262144, 2816]^T, 4-bit (the tied head,
+                        the largest GEMV)
   prefill_chunk         Lq=2048 new queries over 32768 cached keys (4-bit),
                         Hq=32 Hkv=8 D=128, causal
   cpu_baseline          the CPU oracle's decode on the host, bounded sample
@@ -263,6 +265,40 @@ def moe_gather_workload(N, K, E=128, topk=8, B=1, gs=64, bits=4, seed=60, nsets=
     return launch, algo, (parts, idx, xmap, xs, y)
 
 
+# ------------------------------------------------------------- tied head
+
+def tied_head_workload(vocab=262144, H=2816, gs=64, bits=4, seed=80):
+    """QuantizedEmbedding.asLinear at the 26B-A4B table size: x [1, H] @
+    W[vocab, H]^T, 4-bit (415 MB of table, more than the Infinity Cache, so
+    one copy streams from HBM).  A 16384-row block is quantized and copied
+    into every slot of the table."""
+    from mlxq import _lib, ops
+    from mlxq.array import DeviceArray
+
+    blk = 16384
+    src = ops.quantize(rand_t((blk, H), seed, BF16, 0.02), gs, bits)
+    parts = []
+    for a in (src.packed, src.scales, src.biases):
+        full = DeviceArray.empty((vocab,) + a.shape[1:], a.dtype)
+        for r in range(vocab // blk):
+            _lib.call("mlxq_memcpy_dtod", full.ptr + r * a.nbytes, a.ptr, a.nbytes, None)
+        parts.append(full)
+    src.dispose()
+    wp, ws, wb = parts
+    xs = [rand_t((1, H), seed + 1 + i) for i in range(2)]
+    y = DeviceArray.empty((1, vocab), BF16)
+    L = _lib.lib()
+
+    def launch(i):
+        rc = L.mlxq_quantized_matmul(xs[i % 2].ptr, BF16, 1, 1, H, wp.ptr, ws.ptr, wb.ptr, 1, vocab, gs, bits, 1,
+                                     y.ptr, None)
+        if rc:
+            raise RuntimeError(L.mlxq_last_error().decode())
+
+    algo = wp.nbytes + ws.nbytes + wb.nbytes + H * 2 + vocab * 2
+    return launch, algo, (parts, xs, y)
+
+
 # ----------------------------------------------------------------- prefill
 
 def prefill_workload(B=1, Hq=32, Hkv=8, D=128, Lq=2048, N=32768, gs=64, bits=4, seed=7):
@@ -382,6 +418,14 @@ def main():
                          "pct_hbm_peak": round(100 * bm / (msm * 1e-3) / 1e9 / HBM_PEAK_GBS, 1)}
             del km
         extra["moe_gather_decode"] = moe
+        log("bench: tied head")
+        lh, bh, kh = tied_head_workload()
+        msh = timer.graph_step_ms(lh, 50, 5)
+        extra["tied_head_qmv"] = {"workload": "x [1, 2816] @ W[262144, 2816]^T, 4-bit group 64",
+                                  "us_per_call": round(msh * 1e3, 2), "algorithmic_bytes": bh,
+                                  "GB/s": round(bh / (msh * 1e-3) / 1e9, 1),
+                                  "pct_hbm_peak": round(100 * bh / (msh * 1e-3) / 1e9 / HBM_PEAK_GBS, 1)}
+        del kh
         log("bench: chunked prefill")
         l5, f5, k5 = prefill_workload()
         m5, md5 = timer.per_launch_us(l5, 10)

@@ -126,6 +126,19 @@ int mlxq_kv_append(const void* x, int dtype, int64_t heads, int64_t rows_per_hea
 int mlxq_dequantize(const uint32_t* packed, const void* scales, const void* biases, int dtype,
                     int64_t rows, int64_t dim, int group_size, int bits, void* out, void* stream);
 
+/* QuantizedEmbedding.encode -- replaces its three takeAxis gathers of the
+ * packed table, scales and biases plus ops.dequantize
+ * (src/model/gemma4-base.ts:185-194; src/mlx/ops.ts:227-231, :212-225) with
+ * one pass.  ids: [n] uint32 token ids on the device (int32 ids of the same
+ * value are the same bits); table: packed [vocab, dim*bits/32] u32,
+ * scales/biases [vocab, dim/group_size] T.  out: [n, dim] T, row i =
+ * T(scale*code + bias) of table row ids[i]; an id outside [0, vocab) gives a
+ * zero row.  The tied head (QuantizedEmbedding.asLinear, :197-200) is
+ * mlxq_quantized_matmul on the same table. */
+int mlxq_embedding_gather(const uint32_t* ids, int64_t n, const uint32_t* packed, const void* scales,
+                          const void* biases, int dtype, int64_t vocab, int64_t dim, int group_size, int bits,
+                          void* out, void* stream);
+
 /* --------------------------------------------------------- quantized mm */
 
 /* mx.quantized_matmul -- replaces mlx_quantized_matmul as bound by

@@ -135,7 +135,10 @@ __global__ void __launch_bounds__(256) quantize_kernel(const void* __restrict__ 
 template <typename T, int BITS>
 __global__ void __launch_bounds__(256) dequantize_kernel(const uint32_t* __restrict__ packed, const void* __restrict__ scales,
                                                           const void* __restrict__ biases, int64_t rows, int64_t dim,
-                                                          int gs, void* __restrict__ out) {
+                                                          int gs, const uint32_t* __restrict__ ids, int64_t table_rows,
+                                                          void* __restrict__ out) {
+  // out row r dequantizes table row ids[r] (r itself without ids); an id
+  // outside [0, table_rows) gives a zero row
   constexpr int E = 32 / BITS;
   const int64_t words_per_row = dim / E;
   const int64_t total = rows * words_per_row;
@@ -143,13 +146,22 @@ __global__ void __launch_bounds__(256) dequantize_kernel(const uint32_t* __restr
   using S = typename T::storage;
   for (int64_t wi = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; wi < total;
        wi += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t row = wi / words_per_row;
-    const int64_t d0 = (wi % words_per_row) * E;
-    const int64_t gi = row * groups_per_row + d0 / gs;
+    const int64_t row = wi / words_per_row, word = wi % words_per_row;
+    const int64_t d0 = word * E;
+    S* o = reinterpret_cast<S*>(out) + row * dim + d0;
+    int64_t src = row;
+    if (ids) {
+      src = ids[row];
+      if (src >= table_rows) {
+#pragma unroll
+        for (int i = 0; i < E; i++) Conv<T>::store(o, i, 0.f);
+        continue;
+      }
+    }
+    const int64_t gi = src * groups_per_row + d0 / gs;
     const float s = Conv<T>::load(reinterpret_cast<const S*>(scales), gi);
     const float b = Conv<T>::load(reinterpret_cast<const S*>(biases), gi);
-    const uint32_t w = packed[wi];
-    S* o = reinterpret_cast<S*>(out) + row * dim + d0;
+    const uint32_t w = packed[src * words_per_row + word];
 #pragma unroll
     for (int i = 0; i < E; i++) {
       const float c = (float)((w >> (BITS * i)) & ((1u << BITS) - 1u));
@@ -215,6 +227,42 @@ int quantize_impl(const void* x, int dtype, int64_t heads, int64_t rph, int64_t 
 
 }  // namespace
 
+namespace {
+
+int dequantize_impl(const uint32_t* packed, const void* scales, const void* biases, int dtype, int64_t rows,
+                    int64_t dim, int group_size, int bits, const uint32_t* ids, int64_t table_rows, void* out,
+                    void* stream) {
+  int rc = check_quant_args(dtype, dim, group_size, bits);
+  if (rc) return rc;
+  MLXQ_CHECK(rows >= 0, "negative rows");
+  if (rows == 0) return MLXQ_OK;
+  MLXQ_CHECK(packed && scales && biases && out, "null buffer");
+  hipStream_t s = mlxq::resolve_stream(stream);
+  const int64_t words = rows * dim * bits / 32;
+  int64_t blocks = (words + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  MLXQ_DISPATCH_T(dtype, TT, {
+    switch (bits) {
+      case 2:
+        hipLaunchKernelGGL((dequantize_kernel<TT, 2>), dim3((unsigned)blocks), dim3(256), 0, s, packed, scales, biases,
+                           rows, dim, group_size, ids, table_rows, out);
+        break;
+      case 4:
+        hipLaunchKernelGGL((dequantize_kernel<TT, 4>), dim3((unsigned)blocks), dim3(256), 0, s, packed, scales, biases,
+                           rows, dim, group_size, ids, table_rows, out);
+        break;
+      default:
+        hipLaunchKernelGGL((dequantize_kernel<TT, 8>), dim3((unsigned)blocks), dim3(256), 0, s, packed, scales, biases,
+                           rows, dim, group_size, ids, table_rows, out);
+        break;
+    }
+  });
+  MLXQ_LAUNCHED("dequantize_kernel");
+  return MLXQ_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 int mlxq_quantize(const void* w, int dtype, int64_t rows, int64_t dim, int group_size, int bits, uint32_t* packed,
@@ -233,36 +281,21 @@ int mlxq_kv_append(const void* x, int dtype, int64_t heads, int64_t rows_per_hea
                        write_pos % capacity, stream);
 }
 
+
 int mlxq_dequantize(const uint32_t* packed, const void* scales, const void* biases, int dtype, int64_t rows,
                     int64_t dim, int group_size, int bits, void* out, void* stream) {
   MLXQ_REQUIRE_INIT();
-  int rc = check_quant_args(dtype, dim, group_size, bits);
-  if (rc) return rc;
-  MLXQ_CHECK(rows >= 0, "negative rows");
-  if (rows == 0) return MLXQ_OK;
-  MLXQ_CHECK(packed && scales && biases && out, "null buffer");
-  hipStream_t s = mlxq::resolve_stream(stream);
-  const int64_t words = rows * dim * bits / 32;
-  int64_t blocks = (words + 255) / 256;
-  if (blocks > 65536) blocks = 65536;
-  MLXQ_DISPATCH_T(dtype, TT, {
-    switch (bits) {
-      case 2:
-        hipLaunchKernelGGL((dequantize_kernel<TT, 2>), dim3((unsigned)blocks), dim3(256), 0, s, packed, scales, biases,
-                           rows, dim, group_size, out);
-        break;
-      case 4:
-        hipLaunchKernelGGL((dequantize_kernel<TT, 4>), dim3((unsigned)blocks), dim3(256), 0, s, packed, scales, biases,
-                           rows, dim, group_size, out);
-        break;
-      default:
-        hipLaunchKernelGGL((dequantize_kernel<TT, 8>), dim3((unsigned)blocks), dim3(256), 0, s, packed, scales, biases,
-                           rows, dim, group_size, out);
-        break;
-    }
-  });
-  MLXQ_LAUNCHED("dequantize_kernel");
-  return MLXQ_OK;
+  return dequantize_impl(packed, scales, biases, dtype, rows, dim, group_size, bits, nullptr, rows, out, stream);
+}
+
+int mlxq_embedding_gather(const uint32_t* ids, int64_t n, const uint32_t* packed, const void* scales,
+                          const void* biases, int dtype, int64_t vocab, int64_t dim, int group_size, int bits,
+                          void* out, void* stream) {
+  MLXQ_REQUIRE_INIT();
+  MLXQ_CHECK(n >= 0 && vocab >= 0, "negative extent");
+  if (n == 0) return MLXQ_OK;
+  MLXQ_CHECK(ids, "null ids");
+  return dequantize_impl(packed, scales, biases, dtype, n, dim, group_size, bits, ids, vocab, out, stream);
 }
 
 }  // extern "C"
