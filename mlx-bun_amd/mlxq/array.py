@@ -20,16 +20,26 @@ from . import _lib
 class Dtype:
     """mlx_dtype enum values (src/mlx/ffi.ts:297-300)."""
 
+    bool_ = 0
+    uint8 = 1
+    uint16 = 2
     uint32 = 3
+    uint64 = 4
+    int8 = 5
+    int16 = 6
     int32 = 7
+    int64 = 8
     float16 = 9
     float32 = 10
+    float64 = 11
     bfloat16 = 12
 
 
-_ITEMSIZE = {Dtype.uint32: 4, Dtype.int32: 4, Dtype.float16: 2, Dtype.float32: 4, Dtype.bfloat16: 2}
-_NP_STORAGE = {Dtype.uint32: np.uint32, Dtype.int32: np.int32, Dtype.float16: np.uint16,
-               Dtype.float32: np.float32, Dtype.bfloat16: np.uint16}
+_NP_STORAGE = {Dtype.bool_: np.uint8, Dtype.uint8: np.uint8, Dtype.uint16: np.uint16, Dtype.uint32: np.uint32,
+               Dtype.uint64: np.uint64, Dtype.int8: np.int8, Dtype.int16: np.int16, Dtype.int32: np.int32,
+               Dtype.int64: np.int64, Dtype.float16: np.uint16, Dtype.float32: np.float32,
+               Dtype.float64: np.float64, Dtype.bfloat16: np.uint16}
+_ITEMSIZE = {d: np.dtype(t).itemsize for d, t in _NP_STORAGE.items()}
 
 
 def itemsize(dtype: int) -> int:

@@ -60,3 +60,22 @@ def assert_close(got, ref, atol=1e-2, rtol=1e-3, what="", dtype=None):
         i = np.unravel_index(np.argmax(err - tol), err.shape)
         raise AssertionError(f"{what}: {bad.sum()} / {bad.size} elements out of tolerance; worst at {i}: "
                              f"got {got[i]} ref {ref[i]} (max abs err {err.max():.3g})")
+
+
+def write_safetensors(path, tensors, metadata=None):
+    """Write a safetensors file: tensors maps name -> (dtype string, shape,
+    raw bytes) (the format of src/safetensors.ts: u64 LE header length, JSON
+    header, data)."""
+    import json
+    import struct
+
+    header, blobs, off = {}, [], 0
+    if metadata is not None:
+        header["__metadata__"] = metadata
+    for name, (dt, shape, raw) in tensors.items():
+        header[name] = {"dtype": dt, "shape": list(shape), "data_offsets": [off, off + len(raw)]}
+        blobs.append(raw)
+        off += len(raw)
+    hb = json.dumps(header).encode()
+    with open(path, "wb") as f:
+        f.write(struct.pack("<Q", len(hb)) + hb + b"".join(blobs))
