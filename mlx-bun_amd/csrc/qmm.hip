@@ -50,10 +50,14 @@ struct BatchMap {
   }
 };
 
-// weight tiles each qmv wave keeps in flight
-#ifndef QMV_WIN
-#define QMV_WIN 2
-#endif
+// weight tiles each qmv wave keeps in flight: 4 with one MFMA row block
+// (M <= 8: a wave's whole stream of 4 tiles is requested with its x slice,
+// so the tiles do not queue behind the staging wait), 2 with two (register
+// budget)
+template <int MB>
+constexpr int qmv_window() {
+  return MB == 1 ? 4 : 2;
+}
 
 template <typename T, int BITS, int GS, int MB, int R, int TPW, int MR, int XC>
 __global__ void __launch_bounds__(512) qmv_kernel(const uint16_t* __restrict__ x, int M, int K,
@@ -70,6 +74,7 @@ __global__ void __launch_bounds__(512) qmv_kernel(const uint16_t* __restrict__ x
   constexpr int SPL = (SCH + 63) / 64;               // ... per lane
   constexpr int XPW = TPW * TILE_K;                  // x values per row per wave
   constexpr float OFF = CO::OFFSET;
+  constexpr int WIN = qmv_window<MB>();
   static_assert(QG <= 2 && NGW % 4 == 0, "tile / group geometry");
   extern __shared__ __align__(16) uint8_t smem[];
   const int tid = threadIdx.x, lane = tid & 63, nw = blockDim.x >> 6;
@@ -129,7 +134,7 @@ __global__ void __launch_bounds__(512) qmv_kernel(const uint16_t* __restrict__ x
   }
   __builtin_amdgcn_sched_barrier(0);
 
-  // ---- 2. the weight stream: the first QMV_WIN tiles of this wave ----------
+  // ---- 2. the weight stream: the first WIN tiles of this wave --------------
   u32x4_t wr[TPW][R];
   // rows past N sit past the descriptor's end and read 0; the tile offset
   // (inside the row) rides in the scalar offset
@@ -142,7 +147,7 @@ __global__ void __launch_bounds__(512) qmv_kernel(const uint16_t* __restrict__ x
     for (int ri = 0; ri < R; ri++) wr[t][ri] = buf_load128(rw, wlane[ri], toff);
   };
 #pragma unroll
-  for (int t = 0; t < QMV_WIN && t < TPW; t++) issue(t);
+  for (int t = 0; t < WIN && t < TPW; t++) issue(t);
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- 3. this wave's LDS region (no workgroup barrier) -------------------
@@ -186,7 +191,7 @@ __global__ void __launch_bounds__(512) qmv_kernel(const uint16_t* __restrict__ x
 #pragma unroll
     for (int rb = 0; rb < MB; rb++) yacc[ri][rb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  // ---- 4. tiles: compute tile t, then request tile t + QMV_WIN --------------
+  // ---- 4. tiles: compute tile t, then request tile t + WIN ------------------
   // (a clamped duplicate tail tile reads zero x and zero scales: adds nothing)
 #pragma unroll
   for (int t = 0; t < TPW; t++) {
@@ -217,7 +222,7 @@ __global__ void __launch_bounds__(512) qmv_kernel(const uint16_t* __restrict__ x
       }
     }
     __builtin_amdgcn_sched_barrier(0);
-    if (t + QMV_WIN < TPW) issue(t + QMV_WIN);
+    if (t + WIN < TPW) issue(t + WIN);
     __builtin_amdgcn_sched_barrier(0);
     const int gl = t * TILE_K / GS;
 #pragma unroll
