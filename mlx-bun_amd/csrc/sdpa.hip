@@ -814,29 +814,47 @@ __global__ void __launch_bounds__(512) sdpa_prefill_mfma_kernel(
     for (int e = 0; e < 16; e++) oacc[i][e] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
 
+  // Tile t's K/V sit in LDS buffer t & 1; tile t + 1's codes arrive in
+  // registers during tile t - 1 and are staged into the other buffer during
+  // tile t (that buffer's readers passed the previous barrier).  The two
+  // waves sharing a SIMD (w and w + NW/2) take the score MFMAs and the
+  // staging VALU in opposite orders, so one uses the matrix core while the
+  // other dequantizes.  (Alternating the softmax / P V phases as well needs
+  // both orders' live ranges at once and spills.)
   if (kbeg < kend) {
     load(kbeg);
     stash(0);
+    if (kbeg + BN < kend) load(kbeg + BN);
   }
   lds_barrier();
+  const bool mfma_first = wave < NW / 2;
   int buf = 0;
   for (int64_t k0 = kbeg; k0 < kend; k0 += BN) {
     const bool more = k0 + BN < kend;
-    if (more) load(k0 + BN);
     // ---- S^T: two 32-key blocks --------------------------------------------
     f32x16_t sacc[2];
+    auto scores = [&]() {
 #pragma unroll
-    for (int kb = 0; kb < 2; kb++)
+      for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-      for (int e = 0; e < 16; e++) sacc[kb][e] = 0.f;
+        for (int e = 0; e < 16; e++) sacc[kb][e] = 0.f;
 #pragma unroll
-    for (int ks = 0; ks < KS; ks++) {
+      for (int ks = 0; ks < KS; ks++) {
 #pragma unroll
-      for (int kb = 0; kb < 2; kb++) {
-        const u32x4_t a = *reinterpret_cast<const u32x4_t*>(&kt_lds[buf][(32 * kb + lc) * KP + 16 * ks + 8 * lh]);
-        sacc[kb] = mma32<T>(a, qop[ks], sacc[kb]);
+        for (int kb = 0; kb < 2; kb++) {
+          const u32x4_t a = *reinterpret_cast<const u32x4_t*>(&kt_lds[buf][(32 * kb + lc) * KP + 16 * ks + 8 * lh]);
+          sacc[kb] = mma32<T>(a, qop[ks], sacc[kb]);
+        }
       }
+    };
+    if (mfma_first) {
+      scores();
+      if (more) stash(buf ^ 1);
+    } else {
+      if (more) stash(buf ^ 1);
+      scores();
     }
+    if (k0 + 2 * BN < kend) load(k0 + 2 * BN);
     // ---- online softmax over this lane's 32 keys (+ lane ^ 32's) -----------
     // key of sacc[kb][v]: k0 + 32 kb + 8 (v / 4) + 4 lh + v % 4
     const bool need_mask = k0 + BN > valid || (causal && k0 + BN - 1 > wpos_lo) ||
@@ -890,7 +908,6 @@ __global__ void __launch_bounds__(512) sdpa_prefill_mfma_kernel(
         oacc[i] = mma32<T>(a, bop, oacc[i]);
       }
     }
-    if (more) stash(buf ^ 1);
     lds_barrier();
     buf ^= 1;
   }
