@@ -859,12 +859,14 @@ __global__ void __launch_bounds__(512) sdpa_prefill_mfma_kernel(
     // key of sacc[kb][v]: k0 + 32 kb + 8 (v / 4) + 4 lh + v % 4
     const bool need_mask = k0 + BN > valid || (causal && k0 + BN - 1 > wpos_lo) ||
                            (window > 0 && k0 <= valid - Lq + min(Lq - 1, wq_lo + 32) - window);
+    // scores stay in natural units (the running max too); log2(e) enters
+    // each exponent through one fma
     float tmax = -INFINITY;
 #pragma unroll
     for (int kb = 0; kb < 2; kb++)
 #pragma unroll
       for (int v = 0; v < 16; v++) {
-        float sv = sacc[kb][v] * LOG2E;
+        float sv = sacc[kb][v];
         if (need_mask) {  // wave-uniform
           const int64_t j = k0 + 32 * kb + 8 * (v / 4) + 4 * lh + v % 4;
           const bool ok = j < valid && (!causal || j <= pos) && (window <= 0 || pos < j + window) && row_ok;
@@ -875,9 +877,9 @@ __global__ void __launch_bounds__(512) sdpa_prefill_mfma_kernel(
       }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
     const float m_old = m_run;
-    const float m_new = tmax > m_old + 8.0f ? tmax : m_old;  // lazy: p <= 2^8
-    const float alpha = m_new == m_old ? 1.0f : __builtin_amdgcn_exp2f(m_old - m_new);
-    const float m_sub = m_new == -INFINITY ? 0.0f : m_new;
+    const float m_new = tmax > m_old + 8.0f / LOG2E ? tmax : m_old;  // lazy: p <= 2^8
+    const float alpha = m_new == m_old ? 1.0f : __builtin_amdgcn_exp2f((m_old - m_new) * LOG2E);
+    const float m_sub = m_new == -INFINITY ? 0.0f : -m_new * LOG2E;
     m_run = m_new;
     float psum = 0.f;
     uint32_t pk[2][8];  // P as T pairs: [block][pair]
@@ -885,8 +887,8 @@ __global__ void __launch_bounds__(512) sdpa_prefill_mfma_kernel(
     for (int kb = 0; kb < 2; kb++)
 #pragma unroll
       for (int v = 0; v < 16; v += 2) {
-        const float p0 = __builtin_amdgcn_exp2f(sacc[kb][v] - m_sub);
-        const float p1 = __builtin_amdgcn_exp2f(sacc[kb][v + 1] - m_sub);
+        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][v], LOG2E, m_sub));
+        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][v + 1], LOG2E, m_sub));
         psum += p0 + p1;
         pk[kb][v / 2] = Mma<T>::pack2(p0, p1);
       }
