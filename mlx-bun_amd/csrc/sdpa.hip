@@ -173,11 +173,12 @@ struct DecodeShape {
 };
 
 // One workgroup = NW waves = one chunk of up to MAXC keys of one (batch row,
-// kv head).  Wave w owns the 32-key tiles w + NW t, t < TPW.  The chunk's
-// scales/biases are loaded first and staged in LDS as fp32 (per-key
-// constants folded in once per key, not once per MFMA column); codes stream
-// through a WIN-tile register window: tile t + WIN is requested as soon as
-// tile t is consumed, so data arrives while earlier tiles compute.
+// kv head).  Wave w owns the 32-key tiles w + NW t, t < TPW.  Each wave loads
+// its own tiles' scales/biases first and stages them in its LDS region as
+// fp32 (per-key constants folded in once per key, not once per MFMA column;
+// no workgroup barrier, so a wave starts on its first tile as soon as its own
+// data is in); codes stream through a WIN-tile register window: tile t + WIN
+// is requested as soon as tile t is consumed.
 template <typename T, int BITS, int D, int GS>
 __global__ void __launch_bounds__(512) sdpa_decode_mfma_kernel(
     const uint16_t* __restrict__ q, const uint32_t* __restrict__ kp, const uint16_t* __restrict__ ksc,
@@ -186,7 +187,7 @@ __global__ void __launch_bounds__(512) sdpa_decode_mfma_kernel(
     uint16_t* __restrict__ out, float* __restrict__ part_o, float2* __restrict__ part_ml) {
   using CO = CodeOps<T, BITS>;
   using SH = DecodeShape<BITS, D, GS>;
-  constexpr int NW = SH::NW, TPW = SH::TPW, MAXC = SH::MAXC, G = SH::G, KW = SH::KW, WIN = SH::WIN;
+  constexpr int NW = SH::NW, TPW = SH::TPW, G = SH::G, KW = SH::KW, WIN = SH::WIN;
   constexpr int NT = NW * 64;
   constexpr int GW = (G + 1) / 2;    // dwords holding one row's G group values
   constexpr int LKW = KW / 4;        // K-side words per lane (a quarter row)
@@ -196,20 +197,21 @@ __global__ void __launch_bounds__(512) sdpa_decode_mfma_kernel(
   constexpr int E = 32 / BITS;       // codes per word
   constexpr int DT = D / 16;         // V-side MFMA tiles
   constexpr int UMAX = 16 * GS;      // nrep * D <= 16 * GS
-  constexpr int KPT = (MAXC + NT - 1) / NT;  // keys staged per thread
   constexpr float OFF = CO::OFFSET;  // code operands carry +OFF (K and V alike)
   static_assert(VM * E == DT, "tile bookkeeping");
   static_assert(LKW % 4 == 0, "K quarter rows are whole dwordx4 loads");
   static_assert(NT == 512, "launch bounds");
 
-  // sb_lds: [0] K scale * log2e, [1] (K bias - OFF * K scale) * log2e,
-  // [2] V scale, [3] V bias -- per group, per chunk key.  After the tile
-  // loop the same LDS holds u_lds, the per-wave unnormalised outputs
-  // [wave][h*D + d].
-  constexpr int SB_FLOATS = 4 * G * MAXC, U_FLOATS = NW * UMAX;
+  // sb_lds[wave]: [0] K scale * log2e, [1] (K bias - OFF * K scale) * log2e,
+  // [2] V scale, [3] V bias -- per group, for the wave's own keys (tile t at
+  // 32 t): each wave stages and reads only its region, so no workgroup
+  // barrier stands before its first tile.  After the tile loop the same LDS
+  // holds u_lds, the per-wave unnormalised outputs [wave][h*D + d].
+  constexpr int SBW = TPW * 32;  // keys per wave
+  constexpr int SB_FLOATS = NW * 4 * G * SBW, U_FLOATS = NW * UMAX;
   __shared__ float lds_raw[SB_FLOATS > U_FLOATS ? SB_FLOATS : U_FLOATS];
   __shared__ float m_lds[NW][16], l_lds[NW][16];
-  float(&sb_lds)[4][G][MAXC] = *reinterpret_cast<float(*)[4][G][MAXC]>(lds_raw);
+  float(&sb_lds)[NW][4][G][SBW] = *reinterpret_cast<float(*)[NW][4][G][SBW]>(lds_raw);
   float(&u_lds)[NW][UMAX] = *reinterpret_cast<float(*)[NW][UMAX]>(lds_raw);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -256,12 +258,17 @@ __global__ void __launch_bounds__(512) sdpa_decode_mfma_kernel(
                                          make_rsrc(vbi + row0 * G, nk32 * (uint32_t)(2 * G))};
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
 
-  uint32_t sbreg[KPT][4][GW];
+  // this wave's scales/biases: lane l takes key l % 32 of tiles 2p + l / 32
+  // (all four arrays; lanes without a tile read past the descriptors: 0)
+  constexpr int SBP = (TPW + 1) / 2;  // tile pairs
+  const int skey = lane & 31, shalf = lane >> 5;
+  uint32_t sbreg[SBP][4][GW];
 #pragma unroll
-  for (int i = 0; i < KPT; i++) {
-    const uint32_t voff = (uint32_t)(tid + i * NT) * (2 * G);
+  for (int p = 0; p < SBP; p++) {
+    const int t = 2 * p + shalf;
+    const uint32_t voff = t < TPW ? (uint32_t)((wave_u + NW * t) * 32 + skey) * (2 * G) : 0x80000000u;
 #pragma unroll
-    for (int a = 0; a < 4; a++) load_row_groups_buf<G>(rsb[a], voff, 0u, sbreg[i][a]);
+    for (int a = 0; a < 4; a++) load_row_groups_buf<G>(rsb[a], voff, 0u, sbreg[p][a]);
   }
   __builtin_amdgcn_sched_barrier(0);  // issue order: scales/biases, then codes
 
@@ -309,21 +316,19 @@ __global__ void __launch_bounds__(512) sdpa_decode_mfma_kernel(
   for (int t = 0; t < WIN && t < TPW; t++) issue(t, kbuf[t], vbuf[t]);
   __builtin_amdgcn_sched_barrier(0);  // the window is in flight before the first wait
 
-  // ---- stage scales/biases (fp32, per-key constants folded in) ------------
+  // ---- stage this wave's scales/biases (fp32, per-key constants folded in)
 #pragma unroll
-  for (int i = 0; i < KPT; i++) {
-    const int key = tid + i * NT;
-    // (the bound check is compiled only where threads outnumber slots: a
-    // branch here would let the compiler sink the loads behind it)
-    if (MAXC % NT == 0 || key < MAXC) {
+  for (int p = 0; p < SBP; p++) {
+    const int t = 2 * p + shalf;
+    if (TPW % 2 == 0 || t < TPW) {
 #pragma unroll
       for (int g = 0; g < G; g++) {
-        const float ks = Conv<T>::from_bits(group_bits<G>(sbreg[i][0], g));
-        const float kb = Conv<T>::from_bits(group_bits<G>(sbreg[i][1], g));
-        sb_lds[0][g][key] = ks * LOG2E;
-        sb_lds[1][g][key] = (kb - OFF * ks) * LOG2E;
-        sb_lds[2][g][key] = Conv<T>::from_bits(group_bits<G>(sbreg[i][2], g));
-        sb_lds[3][g][key] = Conv<T>::from_bits(group_bits<G>(sbreg[i][3], g));
+        const float ks = Conv<T>::from_bits(group_bits<G>(sbreg[p][0], g));
+        const float kb = Conv<T>::from_bits(group_bits<G>(sbreg[p][1], g));
+        sb_lds[wave_u][0][g][32 * t + skey] = ks * LOG2E;
+        sb_lds[wave_u][1][g][32 * t + skey] = (kb - OFF * ks) * LOG2E;
+        sb_lds[wave_u][2][g][32 * t + skey] = Conv<T>::from_bits(group_bits<G>(sbreg[p][2], g));
+        sb_lds[wave_u][3][g][32 * t + skey] = Conv<T>::from_bits(group_bits<G>(sbreg[p][3], g));
       }
     }
   }
@@ -346,7 +351,6 @@ __global__ void __launch_bounds__(512) sdpa_decode_mfma_kernel(
   qsum = xrow_sum(qsum);
   const uint32_t magic = opaque(Mma<T>::MAGIC);
   const u32x4_t ones = {Mma<T>::ONES, Mma<T>::ONES, Mma<T>::ONES, Mma<T>::ONES};
-  lds_barrier();  // sb_lds ready
 
   // ---- per-wave online softmax state --------------------------------------
   float m_run = -INFINITY;  // per head h_me (log2 domain), replicated over g and lane rows
@@ -359,6 +363,7 @@ __global__ void __launch_bounds__(512) sdpa_decode_mfma_kernel(
 
   auto compute = [&](int t, const uint32_t (&kb)[2][LKW], const uint32_t (&vb)[8][VM]) {
     const int kt = (wave_u + NW * t) * 32;
+    const int st = 32 * t;  // this tile's keys in the wave's sb_lds region
     // scores: two 16-key sub-tiles, D/32 k-steps each
     f32x4_t sacc[2];
 #pragma unroll
@@ -378,10 +383,10 @@ __global__ void __launch_bounds__(512) sdpa_decode_mfma_kernel(
 
     float s2[8];
     {
-      const float4 ka = *reinterpret_cast<const float4*>(&sb_lds[0][g_me][kt + 4 * lg]);
-      const float4 kc = *reinterpret_cast<const float4*>(&sb_lds[0][g_me][kt + 16 + 4 * lg]);
-      const float4 ba = *reinterpret_cast<const float4*>(&sb_lds[1][g_me][kt + 4 * lg]);
-      const float4 bc = *reinterpret_cast<const float4*>(&sb_lds[1][g_me][kt + 16 + 4 * lg]);
+      const float4 ka = *reinterpret_cast<const float4*>(&sb_lds[wave_u][0][g_me][st + 4 * lg]);
+      const float4 kc = *reinterpret_cast<const float4*>(&sb_lds[wave_u][0][g_me][st + 16 + 4 * lg]);
+      const float4 ba = *reinterpret_cast<const float4*>(&sb_lds[wave_u][1][g_me][st + 4 * lg]);
+      const float4 bc = *reinterpret_cast<const float4*>(&sb_lds[wave_u][1][g_me][st + 16 + 4 * lg]);
       const float ks[8] = {ka.x, ka.y, ka.z, ka.w, kc.x, kc.y, kc.z, kc.w};
       const float kd[8] = {ba.x, ba.y, ba.z, ba.w, bc.x, bc.y, bc.z, bc.w};
 #pragma unroll
@@ -418,10 +423,10 @@ __global__ void __launch_bounds__(512) sdpa_decode_mfma_kernel(
     // value-side A operand: row (h_me, g_me) = T(p * s_v); bias term in fp32
     u32x4_t aop;
     {
-      const float4 sa = *reinterpret_cast<const float4*>(&sb_lds[2][g_me][kt + 4 * lg]);
-      const float4 sc = *reinterpret_cast<const float4*>(&sb_lds[2][g_me][kt + 16 + 4 * lg]);
-      const float4 va = *reinterpret_cast<const float4*>(&sb_lds[3][g_me][kt + 4 * lg]);
-      const float4 vc = *reinterpret_cast<const float4*>(&sb_lds[3][g_me][kt + 16 + 4 * lg]);
+      const float4 sa = *reinterpret_cast<const float4*>(&sb_lds[wave_u][2][g_me][st + 4 * lg]);
+      const float4 sc = *reinterpret_cast<const float4*>(&sb_lds[wave_u][2][g_me][st + 16 + 4 * lg]);
+      const float4 va = *reinterpret_cast<const float4*>(&sb_lds[wave_u][3][g_me][st + 4 * lg]);
+      const float4 vc = *reinterpret_cast<const float4*>(&sb_lds[wave_u][3][g_me][st + 16 + 4 * lg]);
       aop.x = Mma<T>::pack2(p[0] * sa.x, p[1] * sa.y);
       aop.y = Mma<T>::pack2(p[2] * sa.z, p[3] * sa.w);
       aop.z = Mma<T>::pack2(p[4] * sc.x, p[5] * sc.y);
