@@ -53,6 +53,11 @@ struct Mma<BF16> {
   __device__ static __forceinline__ uint32_t pack2(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
   }
+  // acc + lo + hi of a packed pair (v_dot2c_f32_bf16 against (1, 1))
+  __device__ static __forceinline__ float sum2(uint32_t pair, float acc) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pair), __builtin_bit_cast(bf16x2_t, ONES), acc,
+                                           false);
+  }
 };
 
 template <>
@@ -66,6 +71,9 @@ struct Mma<F16> {
   }
   __device__ static __forceinline__ uint32_t pack2(float lo, float hi) {  // v_cvt_pk_f16_f32
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, f16x2_t));
+  }
+  __device__ static __forceinline__ float sum2(uint32_t pair, float acc) {  // v_dot2c_f32_f16
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, pair), __builtin_bit_cast(f16x2_t, ONES), acc, false);
   }
 };
 

@@ -630,13 +630,21 @@ __global__ void __launch_bounds__(256) sdpa_decode_merge_kernel(const float4* __
 // runs on the matrix cores.  A workgroup owns 256 query rows of one (batch
 // row, kv head): row r = (query i, head h) with r = i_local * nRep + h, so
 // every head of the kv head shares each K/V tile.  Per 64-key tile:
-//   * K and V codes are dequantized (fp32 s * c + b, rounded to T) into
-//     LDS: K as [key][d], V transposed as [d][key'] with the keys of every
-//     16-key group stored in the order the P operand below produces them;
+//   * K goes to LDS as exact code operands (OFF + c as T, [key][d]) next to
+//     fp32 per-key (s, b - OFF s) of every group; V is dequantized (fp32
+//     s * c + b, rounded to T) and stored transposed as [d][key'] with the
+//     keys of every 16-key group in the order the P operand below produces;
 //   * each wave computes S^T = K Q^T for its 32 rows with
 //     v_mfma_f32_32x32x16 (lane l holds column (query row) l % 32 and 16
-//     keys of each 32-key block), so a row's softmax is in-lane work plus
-//     one exchange with lane l ^ 32;
+//     keys of each 32-key block) as
+//     S^T = sum_g (b - OFF s)_g X_g + sum_g s_g (C_g Q_g^T), X_g the row's
+//     sum of q' over group g: the first sum is one more MFMA per block (the
+//     fp32 b - OFF s and X each split exactly into three truncated bf16
+//     parts, the six products down to 2^-16 of the leading one in the k
+//     slots), the second a chain of code MFMAs per group folded with s in
+//     fp32 -- scores carry no rounding of the dequantized K (at scale 1 and
+//     |q||k| ~ 10 a T-rounded K would move them by ~1e-2); a row's softmax
+//     is in-lane work plus one exchange with lane l ^ 32;
 //   * online softmax in fp32 (lazy rescale), then O^T += V^T P^T where the
 //     P^T operand is exactly the lane's own probabilities packed to T.
 // Next tile's codes are loaded into registers while the current tile
@@ -654,6 +662,18 @@ struct PrefillShape {
   static constexpr int IPT = (KI + VI + NW * 64 - 1) / (NW * 64);  // items per thread
 };
 
+// x = h1 + h2 + h3 exactly: three bf16 truncations (8 significant bits
+// each) of a float and its remainders; returns the bf16 bit patterns.
+__device__ __forceinline__ void split3_bf16(float x, uint32_t& h1, uint32_t& h2, uint32_t& h3) {
+  const uint32_t b1 = __float_as_uint(x) & 0xffff0000u;
+  const float r1 = x - __uint_as_float(b1);
+  const uint32_t b2 = __float_as_uint(r1) & 0xffff0000u;
+  const float r2 = r1 - __uint_as_float(b2);
+  h1 = b1 >> 16;
+  h2 = b2 >> 16;
+  h3 = __float_as_uint(r2) >> 16;
+}
+
 // position of key r (0..15) of a 16-key group in the V^T tile: the P^T
 // operand slot order (quads 1 and 2 swapped)
 __device__ __forceinline__ int vt_pos(int key) { return (key & ~15) | ((key & 4) << 1) | ((key & 8) >> 1) | (key & 3); }
@@ -665,14 +685,23 @@ __global__ void __launch_bounds__(512) sdpa_prefill_mfma_kernel(
     const uint16_t* __restrict__ vbi, int Hq, int Hkv, int Lq, Geometry geo, int causal, int window, float scale,
     uint16_t* __restrict__ out) {
   using SH = PrefillShape<D>;
+  using CO = CodeOps<T, BITS>;
   constexpr int BN = SH::BN, NW = SH::NW, KP = SH::KP, VP = SH::VP, KI = SH::KI, VI = SH::VI, IPT = SH::IPT;
   constexpr int KW = D * BITS / 32;  // code words per cache row
   constexpr int G = D / GS;
   constexpr int KS = D / 16;         // k-steps of S^T
+  constexpr int KPG = GS / 16;       // k-steps per group
   constexpr int DB = D / 32;         // O^T row blocks
   constexpr uint32_t CMASK = (1u << BITS) - 1u;
+  // bias MFMA k slots of group g: 6g .. 6g + 5 = key side [b1 b1 b2 b1 b2 b3],
+  // query side [X1 X2 X1 X3 X2 X1] (b = b - OFF s; 1..3 its exact bf16 parts)
+  constexpr int SPG = 6;
+  constexpr int NBM = (G * SPG + 15) / 16;  // bias MFMAs per 32-key block
+  constexpr int BPP = 16 * NBM + 8;         // bias row pitch (bf16)
   __shared__ __align__(16) uint16_t kt_lds[2][BN * KP];
   __shared__ __align__(16) uint16_t vt_lds[2][D * VP];
+  __shared__ __align__(16) float ks_lds[2][G][BN];           // s per group and key
+  __shared__ __align__(16) uint16_t kbias_lds[2][BN * BPP];  // bias operand rows
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -698,10 +727,14 @@ __global__ void __launch_bounds__(512) sdpa_prefill_mfma_kernel(
   const int wq_lo = min(Lq - 1, (blockIdx.x * SH::ROWS + wave * 32) / nrep);
   const int64_t wpos_lo = valid - Lq + wq_lo;
 
-  // ---- q' = T(q * T(scale)) as the B operand of S^T -----------------------
+  // ---- q' = T(q * T(scale)) as the B operand of S^T (in the code operand's
+  // slot order) and X_g = sum of q' over group g ------------------------------
   const float scale_t = Conv<T>::round(scale);
   const bool apply_scale = scale != 1.0f;
   u32x4_t qop[KS];
+  float xg[G];
+#pragma unroll
+  for (int g = 0; g < G; g++) xg[g] = 0.f;
   {
     const uint16_t* qrow = q + (((int64_t)b * Hq + (int64_t)kvh * nrep + h) * Lq + (row_ok ? qi : 0)) * D;
 #pragma unroll
@@ -715,7 +748,38 @@ __global__ void __launch_bounds__(512) sdpa_prefill_mfma_kernel(
           raw[p2] = Mma<T>::pack2(lo, hi);
         }
       }
-      qop[ks] = raw;
+      float part = 0.f;
+#pragma unroll
+      for (int p2 = 0; p2 < 4; p2++)
+        part += Conv<T>::from_bits(raw[p2] & 0xffffu) + Conv<T>::from_bits(raw[p2] >> 16);
+      xg[ks / KPG] += part;
+      qop[ks] = permute8<CO::ORDER>(raw);
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < G; g++) xg[g] += __shfl_xor(xg[g], 32);
+  // B operand of the bias MFMAs: slot sg = 16 m + 8 lh + e
+  u32x4_t xop[NBM];
+  {
+    uint32_t xs[G][3];
+#pragma unroll
+    for (int g = 0; g < G; g++) split3_bf16(xg[g], xs[g][0], xs[g][1], xs[g][2]);
+    constexpr int PART[SPG] = {0, 1, 0, 2, 1, 0};
+    auto slot = [&](int sg) -> uint32_t { return sg < G * SPG ? xs[sg / SPG][PART[sg % SPG]] : 0u; };
+#pragma unroll
+    for (int m = 0; m < NBM; m++)
+#pragma unroll
+      for (int p2 = 0; p2 < 4; p2++) {
+        const int s0 = 16 * m + 2 * p2;
+        const uint32_t w0 = slot(s0) | (slot(s0 + 1) << 16), w1 = slot(s0 + 8) | (slot(s0 + 9) << 16);
+        xop[m][p2] = lh ? w1 : w0;
+      }
+  }
+  // key-side pad slots G * SPG .. 16 NBM stay zero (staging never writes them)
+  if constexpr (G * SPG < 16 * NBM) {
+    for (int i = tid; i < 2 * BN * (16 * NBM - G * SPG); i += NW * 64) {
+      const int per = 16 * NBM - G * SPG, row = i / per;
+      kbias_lds[row / BN][(row % BN) * BPP + G * SPG + i % per] = 0;
     }
   }
 
@@ -774,19 +838,24 @@ __global__ void __launch_bounds__(512) sdpa_prefill_mfma_kernel(
       const int it = tid + u * NW * 64;
       if (it < KI) {
         const int key = it / (D / 32), qd = it % (D / 32);
-        const float sc = Conv<T>::from_bits(reg_s[u][0]), bi = Conv<T>::from_bits(reg_b[u][0]);
         uint16_t* dst = &kt_lds[buf][key * KP + 32 * qd];
 #pragma unroll
-        for (int j = 0; j < 4; j++) {  // 8 codes -> 8 T values
-          float v[8];
-#pragma unroll
-          for (int e = 0; e < 8; e++) {
-            const int ci = 8 * j + e;  // code index inside the item
-            const uint32_t wv = reg_w[u][ci * BITS / 32];
-            v[e] = __builtin_fmaf(sc, (float)((wv >> ((ci * BITS) % 32)) & CMASK), bi);
-          }
-          *reinterpret_cast<u32x4_t*>(dst + 8 * j) = u32x4_t{Mma<T>::pack2(v[0], v[1]), Mma<T>::pack2(v[2], v[3]),
-                                                             Mma<T>::pack2(v[4], v[5]), Mma<T>::pack2(v[6], v[7])};
+        for (int j = 0; j < 4; j++) {  // 8 codes -> 8 exact operands (OFF + c)
+          if constexpr (BITS == 4)
+            *reinterpret_cast<u32x4_t*>(dst + 8 * j) = CO::operand(reg_w[u][j]);
+          else
+            *reinterpret_cast<u32x4_t*>(dst + 8 * j) = CO::operand(reg_w[u][2 * j], reg_w[u][2 * j + 1]);
+        }
+        if ((32 * qd) % GS == 0) {  // the group's first item writes its s and bias slots
+          const float sc = Conv<T>::from_bits(reg_s[u][0]), bi = Conv<T>::from_bits(reg_b[u][0]);
+          const int g = 32 * qd / GS;
+          ks_lds[buf][g][key] = sc;
+          uint32_t h1, h2, h3;
+          split3_bf16(__builtin_fmaf(-CO::OFFSET, sc, bi), h1, h2, h3);
+          uint32_t* brow = reinterpret_cast<uint32_t*>(&kbias_lds[buf][key * BPP + SPG * g]);
+          brow[0] = h1 | (h1 << 16);
+          brow[1] = h2 | (h1 << 16);
+          brow[2] = h2 | (h3 << 16);
         }
       } else if (it < KI + VI) {
         const int vi = it - KI, kq = vi % (BN / 4), d8 = vi / (BN / 4);
@@ -836,21 +905,51 @@ __global__ void __launch_bounds__(512) sdpa_prefill_mfma_kernel(
   int buf = 0;
   for (int64_t k0 = kbeg; k0 < kend; k0 += BN) {
     const bool more = k0 + BN < kend;
-    // ---- S^T: two 32-key blocks --------------------------------------------
+    // ---- S^T: two 32-key blocks, one group at a time ------------------------
+    // key of sacc[kb][v]: 32 kb + 8 (v / 4) + 4 lh + v % 4 (four consecutive
+    // keys per v / 4, whose (s, b - OFF s) are one 16-byte LDS read each)
     f32x16_t sacc[2];
     auto scores = [&]() {
 #pragma unroll
+      for (int kb = 0; kb < 2; kb++) {
+        f32x16_t acc;
+#pragma unroll
+        for (int e = 0; e < 16; e++) acc[e] = 0.f;
+#pragma unroll
+        for (int m = 0; m < NBM; m++) {
+          const u32x4_t a = *reinterpret_cast<const u32x4_t*>(&kbias_lds[buf][(32 * kb + lc) * BPP + 16 * m + 8 * lh]);
+          acc = mma32<BF16>(a, xop[m], acc);
+        }
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+          // chained MFMAs on one accumulator forward C, so a block's groups
+          // run back to back; only one 16-register partial is live
+          f32x16_t part;
+#pragma unroll
+          for (int e = 0; e < 16; e++) part[e] = 0.f;
+#pragma unroll
+          for (int kk = 0; kk < KPG; kk++) {
+            const int ks = g * KPG + kk;
+            const u32x4_t a = *reinterpret_cast<const u32x4_t*>(&kt_lds[buf][(32 * kb + lc) * KP + 16 * ks + 8 * lh]);
+            part = mma32<T>(a, qop[ks], part);
+          }
+#pragma unroll
+          for (int r4 = 0; r4 < 4; r4++) {
+            const float4 sv = *reinterpret_cast<const float4*>(&ks_lds[buf][g][32 * kb + 8 * r4 + 4 * lh]);
+            acc[4 * r4 + 0] = __builtin_fmaf(sv.x, part[4 * r4 + 0], acc[4 * r4 + 0]);
+            acc[4 * r4 + 1] = __builtin_fmaf(sv.y, part[4 * r4 + 1], acc[4 * r4 + 1]);
+            acc[4 * r4 + 2] = __builtin_fmaf(sv.z, part[4 * r4 + 2], acc[4 * r4 + 2]);
+            acc[4 * r4 + 3] = __builtin_fmaf(sv.w, part[4 * r4 + 3], acc[4 * r4 + 3]);
+          }
+        }
+        sacc[kb] = acc;
+      }
+      // the scores are final here: keeps the fold from being merged with the
+      // other order's copy below the staging (its partials would stay live)
+#pragma unroll
       for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-        for (int e = 0; e < 16; e++) sacc[kb][e] = 0.f;
-#pragma unroll
-      for (int ks = 0; ks < KS; ks++) {
-#pragma unroll
-        for (int kb = 0; kb < 2; kb++) {
-          const u32x4_t a = *reinterpret_cast<const u32x4_t*>(&kt_lds[buf][(32 * kb + lc) * KP + 16 * ks + 8 * lh]);
-          sacc[kb] = mma32<T>(a, qop[ks], sacc[kb]);
-        }
-      }
+        for (int v = 0; v < 16; v++) asm volatile("" : "+v"(sacc[kb][v]));
     };
     if (mfma_first) {
       scores();
@@ -886,7 +985,7 @@ __global__ void __launch_bounds__(512) sdpa_prefill_mfma_kernel(
     const float alpha = m_new == m_old ? 1.0f : __builtin_amdgcn_exp2f((m_old - m_new) * LOG2E);
     const float m_sub = m_new == -INFINITY ? 0.0f : -m_new * LOG2E;
     m_run = m_new;
-    float psum = 0.f;
+    float psum[4] = {0.f, 0.f, 0.f, 0.f};  // four chains: the sum of exactly the P the MFMA sees
     uint32_t pk[2][8];  // P as T pairs: [block][pair]
 #pragma unroll
     for (int kb = 0; kb < 2; kb++)
@@ -894,10 +993,10 @@ __global__ void __launch_bounds__(512) sdpa_prefill_mfma_kernel(
       for (int v = 0; v < 16; v += 2) {
         const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][v], LOG2E, m_sub));
         const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][v + 1], LOG2E, m_sub));
-        psum += p0 + p1;
         pk[kb][v / 2] = Mma<T>::pack2(p0, p1);
+        psum[(v / 2) % 4] = Mma<T>::sum2(pk[kb][v / 2], psum[(v / 2) % 4]);
       }
-    l_run = l_run * alpha + psum;
+    l_run = l_run * alpha + ((psum[0] + psum[1]) + (psum[2] + psum[3]));
     if (__any(alpha != 1.0f)) {
 #pragma unroll
       for (int i = 0; i < DB; i++)

@@ -176,3 +176,41 @@ def test_prefill_full_size_sampled_rows(O, mlxq_dev):
         pre = lambda t: tuple(a[:, :, :n] for a in t)
         ref = O.sdpa(q[:, :, i:i + 1], pre(kq), pre(vq), scale=scale, gs=gs, bits=bits, dtype=BF16)
         assert_close(got[:, :, i:i + 1], ref, what=f"prefill row {i}", dtype=BF16)
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,L,N,D,gs,bits,dtype,window", [
+    (1, 8, 2, 40, 300, 128, 64, 8, BF16, 0),    # 8-bit
+    (2, 4, 4, 17, 129, 128, 32, 4, F16, 0),     # fp16, group 32, no GQA, batch 2
+    (1, 16, 2, 70, 500, 128, 128, 4, BF16, 0),  # group 128, nRep 8
+    (1, 8, 1, 33, 257, 64, 32, 8, F16, 0),      # D = 64
+    (1, 4, 2, 65, 400, 64, 64, 8, BF16, 37),    # D = 64, window
+    (1, 8, 2, 300, 300, 128, 64, 4, F16, 0),    # prompt: queries = all keys
+])
+def test_prefill_mfma_variants(O, mlxq_dev, B, Hq, Hkv, L, N, D, gs, bits, dtype, window):
+    """Every (D, group_size, bits, dtype) instance family of the MFMA prefill
+    kernel against the oracle, bottom-right causal (+ window)."""
+    from mlxq import ops
+
+    q, kq, vq = case(O, B, Hq, Hkv, L, N, D, gs, bits, dtype, 70 + L)
+    mask = ops.createCausalMask(L, N - L, window or None)
+    scale = 1.0 if window else D ** -0.5
+    got = run(O, mlxq_dev, q, kq, vq, dtype, scale, gs, bits, mask=mask)
+    check(O, got, q, kq, vq, dtype, scale, gs, bits, "prefill variant", causal=True, window=window)
+
+
+@pytest.mark.parametrize("Hq,Hkv,L,N,D,gs,bits,dtype", [
+    (8, 2, 70, 600, 128, 64, 4, BF16),
+    (8, 2, 40, 300, 128, 32, 8, F16),   # four groups: two bias MFMAs per block
+    (4, 4, 33, 200, 64, 32, 4, BF16),
+])
+def test_prefill_unscaled_scores(O, mlxq_dev, Hq, Hkv, L, N, D, gs, bits, dtype):
+    """Scale 1 on unit-normal q and k (Gemma4 applies no score scale, its q/k
+    being RMS-normed: src/model/gemma4-base.ts:1282-1285): |q.k| ~ sqrt(D),
+    softmax peaky, so a K dequantized to T before the score product would
+    move scores by ~1e-2 and outputs past the bar; the kernel's scores carry
+    no rounding of K."""
+    from mlxq import ops
+
+    q, kq, vq = case(O, 1, Hq, Hkv, L, N, D, gs, bits, dtype, 90 + L)
+    got = run(O, mlxq_dev, q, kq, vq, dtype, 1.0, gs, bits, mask=ops.createCausalMask(L, N - L, None))
+    check(O, got, q, kq, vq, dtype, 1.0, gs, bits, "prefill scale 1", causal=True)
