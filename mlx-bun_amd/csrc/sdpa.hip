@@ -623,6 +623,334 @@ __global__ void __launch_bounds__(256) sdpa_decode_merge_kernel(const float4* __
   Conv<T>::store(out, o + 3, Ut.w / Lt);
 }
 
+// ===================================================== MFMA decode, wide rows
+//
+// Decode when a kv head's (head, group) pairs exceed the 16 score columns of
+// the kernel above (nRep * D/gs > 16: Gemma4's full-attention layers run
+// 8 query heads per kv head at head_dim 512, src/config.ts:150-156, and only
+// those layers keep a quantized cache, src/model/gemma4-base.ts:414-417).
+// One workgroup = 8 waves = one chunk of keys of one (batch row, kv head),
+// streamed in 128-key tiles:
+//   * scores S = Q K^T on v_mfma_f32_16x16x32 with the heads as rows (A = q',
+//     loaded once) and 16 keys per wave as columns (B = exact code operands
+//     OFF + c straight from memory; lane quarter lq holds codes
+//     [lq gs/4, (lq+1) gs/4) of every group, so a k-step never leaves a
+//     group); per group S += s_k * D + (b_k - OFF s_k) * X_g, s_k and b_k
+//     being per-lane scalars (the column is the key) and X_g the head's sum
+//     of q' over the group -- no rounding of the dequantized K;
+//   * one tile max per head shared through LDS, P = exp2(S - m) written to
+//     LDS as T, the row sum taken over the same T values;
+//   * V dequantized once per tile (fp32 s * c + b -> T) into a transposed
+//     LDS tile, and O += P V with each wave owning D/8 output dims (no
+//     cross-wave output merge);
+//   * the next tile's codes and scales are requested once this one's are
+//     consumed (after the score MFMAs), ahead of its softmax and P V.
+// Chunks write (U, M, L) partials for sdpa_decode_merge_kernel, exactly as
+// the kernel above does.
+template <int D, int GS, int BITS>
+struct WideShape {
+  static constexpr int NW = 8, TK = 128;          // waves, keys per tile (16 per wave)
+  static constexpr int G = D / GS;
+  static constexpr int KW = D * BITS / 32;        // code words per cache row
+  static constexpr int CPQ = GS / 4;              // codes per lane quarter per group
+  static constexpr int WPQ = CPQ * BITS / 32;     // ... as words
+  static constexpr int KST = GS / 32;             // 16x16x32 k-steps per group
+  static constexpr int VTP = TK + 8;              // V^T / P row pitch (T elements)
+  static constexpr int DPW = D / NW;              // output dims per wave
+  static constexpr int CT = DPW / 16;             // 16-dim output column tiles per wave
+  static constexpr int NVI = (TK / 8) * (D / 16); // V staging items (8 keys x 16 dims)
+  static constexpr int VWK = 16 * BITS / 32;      // code words per key of an item
+  static constexpr int GW = (G + 1) / 2;          // dwords per row of G scales
+  static constexpr int MAXC = 1024;
+};
+
+template <typename T, int BITS, int D, int GS>
+__global__ void __launch_bounds__(512) sdpa_decode_wide_kernel(
+    const uint16_t* __restrict__ q, const uint32_t* __restrict__ kp, const uint16_t* __restrict__ ksc,
+    const uint16_t* __restrict__ kbi, const uint32_t* __restrict__ vp, const uint16_t* __restrict__ vsc,
+    const uint16_t* __restrict__ vbi, int Hq, int Hkv, Geometry geo, float scale, int chunk,
+    uint16_t* __restrict__ out, float* __restrict__ part_o, float2* __restrict__ part_ml) {
+  using SH = WideShape<D, GS, BITS>;
+  using CO = CodeOps<T, BITS>;
+  constexpr int NW = SH::NW, TK = SH::TK, G = SH::G, KW = SH::KW, CPQ = SH::CPQ, WPQ = SH::WPQ, KST = SH::KST;
+  constexpr int VTP = SH::VTP, DPW = SH::DPW, CT = SH::CT, NVI = SH::NVI, VWK = SH::VWK, GW = SH::GW;
+  constexpr float OFF = CO::OFFSET;
+  constexpr uint32_t CMASK = (1u << BITS) - 1u;
+  static_assert(G <= 8 && CT >= 1 && NVI <= NW * 64, "wide decode geometry");
+  __shared__ __align__(16) uint16_t vt[D * VTP];  // V^T tile, T
+  __shared__ __align__(16) uint16_t pl[16 * VTP]; // P tile [head][key], T
+  __shared__ float xsum[G][16];                   // X[group][head]
+  __shared__ float tmx[NW][16], lsm[NW][16];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ln = lane & 15, lq = lane >> 4;
+  const int b = blockIdx.z, kvh = blockIdx.y, c = blockIdx.x;
+  const int nslots = gridDim.x;
+  const int nrep = Hq / Hkv;
+  const ChunkRange cr = chunk_range(geo, b, chunk, c);
+  const int64_t out_base = ((int64_t)b * Hq + (int64_t)kvh * nrep) * D;
+  if (cr.nch == 0) {  // nothing to attend: zeros
+    if (c == 0)
+      for (int i = tid; i < nrep * D; i += NW * 64) out[out_base + i] = 0;
+    return;
+  }
+  if (c >= cr.nch) return;
+  const int nk = cr.nk;
+  const int ntiles = (nk + TK - 1) / TK;
+
+  // ---- q' (A operand: row = head ln, k slots of quarter lq) and X ----------
+  const float scale_t = Conv<T>::round(scale);
+  const bool apply_scale = scale != 1.0f;
+  const bool hok = ln < nrep;
+  const uint16_t* qrow = q + out_base + (int64_t)(hok ? ln : 0) * D;
+  u32x4_t qop[G][KST];
+#pragma unroll
+  for (int g = 0; g < G; g++) {
+    float xp = 0.f;
+#pragma unroll
+    for (int s = 0; s < KST; s++) {
+      u32x4_t raw = hok ? *reinterpret_cast<const u32x4_t*>(qrow + g * GS + lq * CPQ + 8 * s) : u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int p2 = 0; p2 < 4; p2++) {
+        const float lo = scaled_q<T>(Conv<T>::from_bits(raw[p2] & 0xffffu), scale_t, apply_scale);
+        const float hi = scaled_q<T>(Conv<T>::from_bits(raw[p2] >> 16), scale_t, apply_scale);
+        raw[p2] = Mma<T>::pack2(lo, hi);
+        xp += lo + hi;
+      }
+      qop[g][s] = permute8<CO::ORDER>(raw);
+    }
+    xp += __shfl_xor(xp, 16);
+    xp += __shfl_xor(xp, 32);
+    if (wave == 0 && lq == 0) xsum[g][ln] = xp;
+  }
+
+  // ---- descriptors (keys past the chunk read 0) ----------------------------
+  const int64_t row0 = ((int64_t)b * Hkv + kvh) * geo.cap + cr.slot0;
+  const uint32_t nk32 = (uint32_t)nk;
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kp + row0 * KW, nk32 * (uint32_t)(KW * 4));
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vp + row0 * KW, nk32 * (uint32_t)(KW * 4));
+  const __amdgpu_buffer_rsrc_t rks = make_rsrc(ksc + row0 * G, nk32 * (uint32_t)(2 * G));
+  const __amdgpu_buffer_rsrc_t rkb = make_rsrc(kbi + row0 * G, nk32 * (uint32_t)(2 * G));
+  const __amdgpu_buffer_rsrc_t rvs = make_rsrc(vsc + row0 * G, nk32 * (uint32_t)(2 * G));
+  const __amdgpu_buffer_rsrc_t rvb = make_rsrc(vbi + row0 * G, nk32 * (uint32_t)(2 * G));
+
+  // K side of a tile: lane (key ln of this wave's 16, quarter lq)
+  struct KSlot {
+    uint32_t w[G][WPQ];
+    uint32_t s[GW], bb[GW];
+  };
+  // V side: item it = tid (key octet it % 16 fastest, 16-dim block it / 16)
+  struct VSlot {
+    uint32_t w[8][VWK];
+    uint32_t s[8], bb[8];  // the dword holding each key's scale / bias of the block's group
+  };
+  const bool vact = tid < NVI;
+  const int ko = tid % 16, db = tid / 16;
+  const int vg = (16 * db) / GS;
+  auto load_k = [&](int t, KSlot& k) {
+    const uint32_t key = (uint32_t)(TK * t + 16 * wave + ln);
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+      const uint32_t off = (key * KW + (uint32_t)g * (GS * BITS / 32) + (uint32_t)lq * WPQ) * 4u;
+      if constexpr (WPQ == 1) {
+        k.w[g][0] = buf_load32(rk, off, 0u);
+      } else if constexpr (WPQ == 2) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(rk, (int)off, 0, 0);
+        k.w[g][0] = v[0];
+        k.w[g][1] = v[1];
+      } else {
+#pragma unroll
+        for (int h = 0; h < WPQ / 4; h++) {
+          const u32x4_t v = buf_load128(rk, off + 16u * h, 0u);
+          k.w[g][4 * h] = v.x;
+          k.w[g][4 * h + 1] = v.y;
+          k.w[g][4 * h + 2] = v.z;
+          k.w[g][4 * h + 3] = v.w;
+        }
+      }
+    }
+    load_row_groups_buf<G>(rks, key * (uint32_t)(2 * G), 0u, k.s);
+    load_row_groups_buf<G>(rkb, key * (uint32_t)(2 * G), 0u, k.bb);
+  };
+  auto load_v = [&](int t, VSlot& v) {
+#pragma unroll
+    for (int kk = 0; kk < 8; kk++) {
+      const uint32_t key = (uint32_t)(TK * t + 8 * ko + kk);
+      const uint32_t off = vact ? (key * KW + (uint32_t)db * VWK) * 4u : 0x80000000u;  // inactive: reads 0
+      if constexpr (VWK == 2) {
+        const auto x = __builtin_amdgcn_raw_buffer_load_b64(rv, (int)off, 0, 0);
+        v.w[kk][0] = x[0];
+        v.w[kk][1] = x[1];
+      } else {
+        const u32x4_t x = buf_load128(rv, off, 0u);
+        v.w[kk][0] = x.x;
+        v.w[kk][1] = x.y;
+        v.w[kk][2] = x.z;
+        v.w[kk][3] = x.w;
+      }
+      const uint32_t so = vact ? ((key * (uint32_t)G + (uint32_t)vg) * 2u) & ~3u : 0x80000000u;
+      v.s[kk] = __builtin_amdgcn_raw_buffer_load_b32(rvs, (int)so, 0, 0);
+      v.bb[kk] = __builtin_amdgcn_raw_buffer_load_b32(rvb, (int)so, 0, 0);
+    }
+  };
+  // V: s * c + b -> T, written as V^T rows (16 dims) of 8 keys
+  auto stage_v = [&](int t, const VSlot& v) {
+    if (!vact) return;
+    const int sh = 16 * (int)((((uint32_t)(TK * t + 8 * ko) * (uint32_t)G + (uint32_t)vg)) & 1u);
+    float sc[8], bi[8];
+#pragma unroll
+    for (int kk = 0; kk < 8; kk++) {  // G * key + vg has the parity of vg for even G
+      const int shk = (G % 2 == 0) ? sh : 16 * (int)((((uint32_t)(TK * t + 8 * ko + kk) * (uint32_t)G + (uint32_t)vg)) & 1u);
+      sc[kk] = Conv<T>::from_bits((v.s[kk] >> shk) & 0xffffu);
+      bi[kk] = Conv<T>::from_bits((v.bb[kk] >> shk) & 0xffffu);
+    }
+#pragma unroll
+    for (int e = 0; e < 16; e++) {
+      float x[8];
+#pragma unroll
+      for (int kk = 0; kk < 8; kk++) {
+        const uint32_t wv = v.w[kk][e * BITS / 32];
+        x[kk] = __builtin_fmaf(sc[kk], (float)((wv >> ((e * BITS) % 32)) & CMASK), bi[kk]);
+      }
+      *reinterpret_cast<u32x4_t*>(&vt[(16 * db + e) * VTP + 8 * ko]) =
+          u32x4_t{Mma<T>::pack2(x[0], x[1]), Mma<T>::pack2(x[2], x[3]), Mma<T>::pack2(x[4], x[5]),
+                  Mma<T>::pack2(x[6], x[7])};
+    }
+  };
+
+  // ---- online softmax state: rows 4 lq + i (heads) of the 16x16 layouts ----
+  float m_run[4], l_run[4];
+  f32x4_t oacc[CT];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    m_run[i] = -INFINITY;
+    l_run[i] = 0.f;
+  }
+#pragma unroll
+  for (int ct = 0; ct < CT; ct++) oacc[ct] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const uint32_t magic = opaque(Mma<T>::MAGIC);
+
+  // one register slot each: a tile consumes its codes (V staging, score
+  // MFMAs) before the next tile's loads refill the same slots
+  auto tile = [&](int t, KSlot& k, VSlot& v) {
+    stage_v(t, v);
+    // scores of this wave's 16 keys, log2 units
+    f32x4_t sacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+      f32x4_t part = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < KST; s++) {
+        u32x4_t bop;
+        if constexpr (BITS == 4)
+          bop = CodeOps<T, 4>::operand(k.w[g][s], magic);
+        else
+          bop = CodeOps<T, BITS>::operand(k.w[g][2 * s], k.w[g][2 * s + 1]);
+        part = Mma<T>::mma(qop[g][s], bop, part);
+      }
+      const float ks = Conv<T>::from_bits(group_bits<G>(k.s, g));
+      const float kd = (Conv<T>::from_bits(group_bits<G>(k.bb, g)) - OFF * ks) * LOG2E;
+      const float4 xv = *reinterpret_cast<const float4*>(&xsum[g][4 * lq]);
+      const float xa[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+      for (int i = 0; i < 4; i++) sacc[i] = __builtin_fmaf(ks * LOG2E, part[i], __builtin_fmaf(kd, xa[i], sacc[i]));
+    }
+    const bool key_ok = TK * t + 16 * wave + ln < nk;
+    float tmax[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      sacc[i] = key_ok ? sacc[i] : -INFINITY;
+      float mv = sacc[i];
+      mv = fmaxf(mv, __shfl_xor(mv, 1));
+      mv = fmaxf(mv, __shfl_xor(mv, 2));
+      mv = fmaxf(mv, __shfl_xor(mv, 4));
+      mv = fmaxf(mv, __shfl_xor(mv, 8));
+      tmax[i] = mv;
+    }
+    if (ln == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) tmx[wave][4 * lq + i] = tmax[i];
+    }
+    if (t + 1 < ntiles) {  // workgroup-uniform
+      load_k(t + 1, k);
+      load_v(t + 1, v);
+    }
+    lds_barrier();  // tile maxima and V^T in
+    float alpha[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      float tm = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < NW; w++) tm = fmaxf(tm, tmx[w][4 * lq + i]);
+      const float m_old = m_run[i];
+      const float m_new = tm > m_old + 8.0f ? tm : m_old;  // lazy: p <= 2^8
+      alpha[i] = m_new == m_old ? 1.0f : __builtin_amdgcn_exp2f(m_old - m_new);
+      m_run[i] = m_new;
+      const float msub = m_new == -INFINITY ? 0.f : m_new;
+      const uint32_t pb = Conv<T>::to_bits(__builtin_amdgcn_exp2f(sacc[i] - msub));
+      pl[(4 * lq + i) * VTP + 16 * wave + ln] = (uint16_t)pb;
+      l_run[i] = l_run[i] * alpha[i] + Conv<T>::from_bits(pb);  // the P the MFMA sees
+    }
+    if (__any(alpha[0] != 1.0f || alpha[1] != 1.0f || alpha[2] != 1.0f || alpha[3] != 1.0f)) {
+#pragma unroll
+      for (int ct = 0; ct < CT; ct++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) oacc[ct][i] *= alpha[i];
+    }
+    lds_barrier();  // P in
+#pragma unroll
+    for (int kq = 0; kq < TK / 32; kq++) {
+      const u32x4_t a = *reinterpret_cast<const u32x4_t*>(&pl[ln * VTP + 32 * kq + 8 * lq]);
+#pragma unroll
+      for (int ct = 0; ct < CT; ct++) {
+        const u32x4_t bv = *reinterpret_cast<const u32x4_t*>(&vt[(DPW * wave + 16 * ct + ln) * VTP + 32 * kq + 8 * lq]);
+        oacc[ct] = Mma<T>::mma(a, bv, oacc[ct]);
+      }
+    }
+    lds_barrier();  // the tile's V^T and P are free again
+  };
+
+  KSlot kslot;
+  VSlot vslot;
+  load_k(0, kslot);
+  load_v(0, vslot);
+  lds_barrier();  // X in
+  for (int t = 0; t < ntiles; t++) tile(t, kslot, vslot);
+
+  // ---- row sums over keys (lanes) and waves; store -------------------------
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    float lv = l_run[i];
+    lv += __shfl_xor(lv, 1);
+    lv += __shfl_xor(lv, 2);
+    lv += __shfl_xor(lv, 4);
+    lv += __shfl_xor(lv, 8);
+    if (ln == 0) lsm[wave][4 * lq + i] = lv;
+  }
+  lds_barrier();
+  const bool single = cr.nch == 1;
+  const int64_t pc = ((int64_t)b * Hkv + kvh) * nslots + c;  // this chunk's partial slot
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int h = 4 * lq + i;
+    if (h < nrep) {
+      float L = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; w++) L += lsm[w][h];
+#pragma unroll
+      for (int ct = 0; ct < CT; ct++) {
+        const int d = DPW * wave + 16 * ct + ln;
+        if (single)
+          Conv<T>::store(out, out_base + (int64_t)h * D + d, oacc[ct][i] / L);
+        else
+          part_o[(pc * nrep + h) * D + d] = oacc[ct][i];
+      }
+      if (!single && wave == 0 && ln == 0) part_ml[pc * nrep + h] = make_float2(m_run[i], L);
+    }
+  }
+}
+
 // ========================================================== MFMA prefill
 //
 // Lq > 1 (chunked prefill over the quantized cache, quantizedSdpaTiled's
@@ -1233,6 +1561,77 @@ int launch_decode_d(int D, int gs, const void* q, int B, int Hq, int Hkv, const 
   return mlxq::fail(MLXQ_ERR_UNSUPPORTED, "decode: no MFMA instance for this head_dim/group_size");
 }
 
+template <typename T, int BITS, int D, int GS>
+int launch_decode_wide(const void* q, int B, int Hq, int Hkv, const uint32_t* kp, const void* ks, const void* kb,
+                       const uint32_t* vp, const void* vs, const void* vb, Geometry geo, float scale, void* out,
+                       hipStream_t s) {
+  using SH = WideShape<D, GS, BITS>;
+  MLXQ_CHECK(geo.cap * (int64_t)SH::KW * 4 < ((int64_t)1 << 31), "kv cache rows too long for one launch");
+  const int64_t span = geo.valid_len ? geo.cap : geo.n_kv;  // per-row upper bound on keys
+  int chunk = SH::MAXC;
+  const int ov = decode_chunk_override();
+  if (ov >= SH::TK && ov <= SH::MAXC && (ov & (ov - 1)) == 0) {
+    chunk = ov;
+  } else {
+    const int64_t cus = mlxq::device_cu_count();
+    while (chunk > SH::TK && ((span + chunk - 1) / chunk) * B * Hkv < cus) chunk /= 2;
+  }
+  const int64_t nchunks = (span > 0 ? (span + chunk - 1) / chunk : 1) + (geo.ring_off ? 1 : 0);
+  MLXQ_CHECK(nchunks < 65536, "kv length too large for one launch");
+  void* pws = nullptr;
+  const int nrep = Hq / Hkv;
+  const size_t slots = (size_t)B * Hkv * nchunks;
+  const size_t obytes = (slots * nrep * D * sizeof(float) + 255) & ~(size_t)255;
+  const size_t pbytes = nchunks > 1 ? obytes + slots * nrep * sizeof(float2) : 0;
+  if (pbytes) {
+    uint32_t* unused_counters = nullptr;
+    int rc = mlxq::workspace(pbytes, 0, &unused_counters, &pws, s);
+    if (rc) return rc;
+  }
+  float* part_o = (float*)pws;
+  float2* part_ml = pbytes ? (float2*)((uint8_t*)pws + obytes) : nullptr;
+  dim3 grid((unsigned)nchunks, (unsigned)Hkv, (unsigned)B);
+  hipLaunchKernelGGL((sdpa_decode_wide_kernel<T, BITS, D, GS>), grid, dim3(SH::NW * 64), 0, s, (const uint16_t*)q,
+                     kp, (const uint16_t*)ks, (const uint16_t*)kb, vp, (const uint16_t*)vs, (const uint16_t*)vb, Hq,
+                     Hkv, geo, scale, chunk, (uint16_t*)out, part_o, part_ml);
+  MLXQ_LAUNCHED("sdpa_decode_wide_kernel");
+  if (nchunks > 1) {
+    const int cols = nrep * D / 4;
+    dim3 mgrid((unsigned)((cols + 63) / 64), (unsigned)Hkv, (unsigned)B);
+    hipLaunchKernelGGL((sdpa_decode_merge_kernel<T>), mgrid, dim3(256), 0, s, (const float4*)part_o, part_ml, Hq,
+                       Hkv, D, geo, chunk, (int)nchunks, (uint16_t*)out);
+    MLXQ_LAUNCHED("sdpa_decode_merge_kernel");
+  }
+  return MLXQ_OK;
+}
+
+template <typename T, int BITS>
+int launch_decode_wide_d(int D, int gs, const void* q, int B, int Hq, int Hkv, const uint32_t* kp, const void* ks,
+                         const void* kb, const uint32_t* vp, const void* vs, const void* vb, Geometry geo,
+                         float scale, void* out, hipStream_t s) {
+#define WDEC(DV, GV)                                                                                            \
+  if (D == DV && gs == GV)                                                                                      \
+    return launch_decode_wide<T, BITS, DV, GV>(q, B, Hq, Hkv, kp, ks, kb, vp, vs, vb, geo, scale, out, s);
+  WDEC(128, 32) WDEC(128, 64) WDEC(128, 128)
+  WDEC(256, 32) WDEC(256, 64) WDEC(256, 128)
+  WDEC(512, 64) WDEC(512, 128)
+#undef WDEC
+  return mlxq::fail(MLXQ_ERR_UNSUPPORTED, "decode: no wide MFMA instance for this head_dim/group_size");
+}
+
+// The wide decode kernel: up to 16 query heads per kv head, at most 8
+// quant groups per row (one row's K scales are one 2G-byte load; V scales
+// are read as aligned dwords).
+bool decode_wide_ok(int dtype, int bits, int D, int gs, int nrep, std::initializer_list<const void*> sb) {
+  if (!mlxq::is_half_dtype(dtype)) return false;
+  if (bits != 4 && bits != 8) return false;
+  if (!(D == 128 || D == 256 || (D == 512 && gs >= 64))) return false;
+  const uintptr_t al = 2 * (D / gs) > 4 ? 2 * (D / gs) : 4;
+  for (const void* p : sb)
+    if ((uintptr_t)p % al) return false;
+  return nrep <= 16;
+}
+
 // The MFMA decode kernel reads a cache row's G = D/gs scales (biases) with
 // one 2G-byte load, so those arrays must be 2G-byte aligned.
 bool decode_mfma_ok(int dtype, int bits, int D, int gs, int nrep, std::initializer_list<const void*> sb) {
@@ -1284,6 +1683,17 @@ extern "C" int mlxq_quantized_sdpa(const void* q, int dtype, int B, int Hq, int 
                                                v_scales, v_biases, geo, scale, out, s)
                      : launch_decode_d<F16, 8>(D, group_size, q, B, Hq, Hkv, k_packed, k_scales, k_biases, v_packed,
                                                v_scales, v_biases, geo, scale, out, s);
+  }
+  if (decode && decode_wide_ok(dtype, bits, D, group_size, nrep, {k_scales, k_biases, v_scales, v_biases})) {
+    if (dtype == MLXQ_BFLOAT16)
+      return bits == 4 ? launch_decode_wide_d<BF16, 4>(D, group_size, q, B, Hq, Hkv, k_packed, k_scales, k_biases,
+                                                       v_packed, v_scales, v_biases, geo, scale, out, s)
+                       : launch_decode_wide_d<BF16, 8>(D, group_size, q, B, Hq, Hkv, k_packed, k_scales, k_biases,
+                                                       v_packed, v_scales, v_biases, geo, scale, out, s);
+    return bits == 4 ? launch_decode_wide_d<F16, 4>(D, group_size, q, B, Hq, Hkv, k_packed, k_scales, k_biases,
+                                                    v_packed, v_scales, v_biases, geo, scale, out, s)
+                     : launch_decode_wide_d<F16, 8>(D, group_size, q, B, Hq, Hkv, k_packed, k_scales, k_biases,
+                                                    v_packed, v_scales, v_biases, geo, scale, out, s);
   }
   const int causal = mask_mode == MLXQ_MASK_CAUSAL;
   // Lq > 1 on the matrix cores: plain (non-ring) caches, T = bf16/f16, 4/8-bit

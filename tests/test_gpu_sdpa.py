@@ -96,13 +96,41 @@ def test_decode_shapes(O, mlxq_dev, B, Hq, Hkv, N, D, gs, bits, dtype):
 
 
 @pytest.mark.parametrize("B,Hq,Hkv,N,D,gs,bits,dtype", [
-    (1, 16, 1, 333, 512, 64, 4, BF16),    # the 12B full-attention site (nRep 16, D 512)
+    (1, 32, 1, 150, 128, 64, 4, BF16),    # nRep 32: past the MFMA kernels' 16 head rows
     (1, 4, 2, 200, 128, 64, 2, BF16),     # 2-bit
     (1, 4, 2, 150, 128, 64, 4, F32),      # fp32 activations
 ])
 def test_decode_generic_shapes(O, mlxq_dev, B, Hq, Hkv, N, D, gs, bits, dtype):
     q, kq, vq = case(O, B, Hq, Hkv, 1, N, D, gs, bits, dtype, 9)
     check(O, run(O, mlxq_dev, q, kq, vq, dtype, 1.0, gs, bits), q, kq, vq, dtype, 1.0, gs, bits, "generic")
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,N,D,gs,bits,dtype,scale", [
+    (1, 16, 2, 4096, 512, 64, 4, BF16, 1.0),    # Gemma4 full attention (src/config.ts:150-156): nRep 8, D 512
+    (1, 16, 1, 333, 512, 64, 4, BF16, 1.0),     # the 12B full-attention site: nRep 16
+    (2, 16, 2, 1000, 512, 128, 8, F16, 1.0),    # group 128, 8-bit
+    (1, 16, 2, 777, 256, 32, 4, BF16, 0.0625),  # nRep 8 x 8 groups at D 256
+    (1, 32, 2, 3000, 128, 64, 8, BF16, 0.125),  # nRep 16 at D 128
+    (1, 8, 1, 100, 512, 64, 4, F16, 1.0),       # one chunk: outputs written by the kernel itself
+    (1, 16, 2, 33001, 512, 64, 4, BF16, 1.0),   # 32k context, ragged last tile
+])
+def test_decode_wide(O, mlxq_dev, B, Hq, Hkv, N, D, gs, bits, dtype, scale):
+    """Decode with more (head, group) score columns than one 16-wide MFMA
+    tile holds: the wide kernel (heads as MFMA rows, exact K operands, V
+    dequantized through LDS) against the fp64 oracle."""
+    q, kq, vq = case(O, B, Hq, Hkv, 1, N, D, gs, bits, dtype, N + 1)
+    check(O, run(O, mlxq_dev, q, kq, vq, dtype, scale, gs, bits), q, kq, vq, dtype, scale, gs, bits, "wide")
+
+
+def test_decode_wide_ring(O, mlxq_dev):
+    """Rotating rows at the Gemma4 full-attention shape: per-row valid lengths
+    (short, one short of the ring, full, wrapped past it) and ring offsets."""
+    B, W = 4, 2048
+    lens = np.array([100, 2047, 2048, 5000], np.int32)
+    ring = np.random.default_rng(8).integers(0, W, B).astype(np.int32)
+    q, kq, vq = case(O, B, 16, 2, 1, W, 512, 64, 4, BF16, 21)
+    got = run(O, mlxq_dev, q, kq, vq, BF16, 1.0, 64, 4, valid=lens, ring=ring)
+    check(O, got, q, kq, vq, BF16, 1.0, 64, 4, "wide ring", valid_len=lens, ring_off=ring)
 
 
 def test_decode_empty_rows_are_zero(O, mlxq_dev):
