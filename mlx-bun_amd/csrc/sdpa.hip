@@ -1362,6 +1362,339 @@ __global__ void __launch_bounds__(512) sdpa_prefill_mfma_kernel(
   }
 }
 
+// ===================================================== MFMA prefill, wide rows
+//
+// Lq > 1 at head_dim 256 / 512 (Gemma4's full-attention layers, the only
+// ones with a quantized cache): the kernel above keeps a 32-row block's whole
+// output (D/32 accumulator tiles) and q' (D/16 operands) in registers, which
+// does not fit past D = 128.  Here a wave owns 16 (query, head) rows as the
+// rows of v_mfma_f32_16x16x32 (4 waves, one per SIMD: its D/16 accumulator
+// tiles and q' operands take most of a SIMD's registers).
+// Per 32-key tile, shared by the workgroup through a double-buffered LDS:
+//   * K as exact code operands OFF + c plus fp32 per-key (s, b - OFF s); the
+//     scores S = s (C q'^T) + (b - OFF s) X per group (lane quarter lq holds
+//     codes [lq gs/4, (lq+1) gs/4) of each group), no rounding of K;
+//   * V dequantized (fp32 s * c + b -> T) and transposed;
+//   * online softmax per row (natural units, log2(e) in each exponent),
+//     causal / window masks on boundary tiles only;
+//   * P goes through the wave's own LDS rows into the A operand of O += P V
+//     (no barrier: a wave's LDS accesses stay in order).
+template <int D, int GS, int BITS>
+struct PrefillWideShape {
+  static constexpr int NW = 4;                    // waves (16 rows each), one per SIMD
+  static constexpr int ROWS = 16 * NW;
+  static constexpr int NT = NW * 64;
+  static constexpr int TK = 32;                   // keys per tile
+  static constexpr int G = D / GS;
+  static constexpr int KW = D * BITS / 32;        // code words per cache row
+  static constexpr int CPQ = GS / 4, KST = GS / 32;
+  static constexpr int KP = D + 8;                // K tile pitch (T)
+  static constexpr int VP = TK + 8;               // V^T / P pitch (T)
+  static constexpr int UW = BITS / 4;             // code words per 8-code unit
+  static constexpr int KIT = TK * D / 8 / NT;     // K units (8 codes) per thread per tile
+  static constexpr int VI = (TK / 8) * (D / 8);   // V items: 8 keys x 8 dims
+  static constexpr int SI = TK * G;               // K (s, b) items
+  static constexpr int DC = D / 16;               // output column tiles
+};
+
+template <typename T, int BITS, int D, int GS>
+__global__ void __launch_bounds__(256) sdpa_prefill_wide_kernel(
+    const uint16_t* __restrict__ q, const uint32_t* __restrict__ kp, const uint16_t* __restrict__ ksc,
+    const uint16_t* __restrict__ kbi, const uint32_t* __restrict__ vp, const uint16_t* __restrict__ vsc,
+    const uint16_t* __restrict__ vbi, int Hq, int Hkv, int Lq, Geometry geo, int causal, int window, float scale,
+    uint16_t* __restrict__ out) {
+  using SH = PrefillWideShape<D, GS, BITS>;
+  using CO = CodeOps<T, BITS>;
+  constexpr int NW = SH::NW, ROWS = SH::ROWS, NT = SH::NT, TK = SH::TK, G = SH::G, KW = SH::KW, CPQ = SH::CPQ;
+  constexpr int KST = SH::KST, KP = SH::KP, VP = SH::VP, UW = SH::UW, KIT = SH::KIT, VI = SH::VI, SI = SH::SI;
+  constexpr int DC = SH::DC;
+  constexpr float OFF = CO::OFFSET;
+  constexpr uint32_t CMASK = (1u << BITS) - 1u;
+  static_assert(KIT >= 1 && VI <= NT && SI <= NT && G <= 8 && NT == 256, "wide prefill geometry");
+  __shared__ __align__(16) uint16_t kt_lds[2][TK * KP];
+  __shared__ __align__(16) uint16_t vt_lds[2][D * VP];
+  __shared__ __align__(16) float ksb[2][2][G][TK];  // [buf][s | b - OFF s][group][key]
+  __shared__ __align__(16) uint16_t pw[NW][16 * VP];  // each wave's P rows
+  __shared__ __align__(16) float xw[NW][G][16];       // each wave's X[group][row]
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ln = lane & 15, lq = lane >> 4;
+  const int b = blockIdx.z, kvh = blockIdx.y;
+  const int nrep = Hq / Hkv;
+  const int64_t valid = row_valid(geo, b);
+  const int64_t rowbase = ((int64_t)b * Hkv + kvh) * geo.cap;
+
+  // ---- rows: r = query * nrep + head; the A operand's row is ln, the
+  // accumulator rows are 4 lq + i --------------------------------------------
+  const int r0 = blockIdx.x * ROWS + 16 * wave;
+  int64_t pos[4];
+  bool rok[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int r = r0 + 4 * lq + i, qi = r / nrep;
+    rok[i] = qi < Lq;
+    pos[i] = valid - Lq + (rok[i] ? qi : Lq - 1);
+  }
+  const int qi_lo = blockIdx.x * ROWS / nrep;
+  const int qi_hi = min(Lq - 1, (blockIdx.x * ROWS + ROWS - 1) / nrep);
+  int64_t kend = valid, kbeg = 0;
+  if (causal) kend = min(kend, valid - Lq + qi_hi + 1);
+  if (window > 0) kbeg = max((int64_t)0, valid - Lq + qi_lo - window + 1);
+  kbeg = kbeg / TK * TK;
+  const int wq_lo = min(Lq - 1, r0 / nrep), wq_hi = min(Lq - 1, (r0 + 15) / nrep);
+  const int64_t wpos_lo = valid - Lq + wq_lo, wpos_hi = valid - Lq + wq_hi;
+
+  // ---- q' operand (row ln, quarter lq) and X[group][row] -------------------
+  const float scale_t = Conv<T>::round(scale);
+  const bool apply_scale = scale != 1.0f;
+  u32x4_t qop[G][KST];
+  {
+    const int ra = r0 + ln, qa = ra / nrep, ha = ra % nrep;
+    const bool aok = qa < Lq;
+    const uint16_t* qrow = q + (((int64_t)b * Hq + (int64_t)kvh * nrep + ha) * Lq + (aok ? qa : 0)) * D;
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+      float xp = 0.f;
+#pragma unroll
+      for (int s = 0; s < KST; s++) {
+        u32x4_t raw = aok ? *reinterpret_cast<const u32x4_t*>(qrow + g * GS + lq * CPQ + 8 * s) : u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int p2 = 0; p2 < 4; p2++) {
+          const float lo = scaled_q<T>(Conv<T>::from_bits(raw[p2] & 0xffffu), scale_t, apply_scale);
+          const float hi = scaled_q<T>(Conv<T>::from_bits(raw[p2] >> 16), scale_t, apply_scale);
+          raw[p2] = Mma<T>::pack2(lo, hi);
+          xp += lo + hi;
+        }
+        qop[g][s] = permute8<CO::ORDER>(raw);
+      }
+      xp += __shfl_xor(xp, 16);
+      xp += __shfl_xor(xp, 32);
+      if (lq == 0) xw[wave][g][ln] = xp;
+    }
+  }
+
+  // ---- K/V tile staging (raw buffer loads bounded to the valid keys) --------
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kp + rowbase * KW, (uint32_t)(valid * KW * 4));
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vp + rowbase * KW, (uint32_t)(valid * KW * 4));
+  const __amdgpu_buffer_rsrc_t rks = make_rsrc(ksc + rowbase * G, (uint32_t)(valid * G * 2));
+  const __amdgpu_buffer_rsrc_t rkb = make_rsrc(kbi + rowbase * G, (uint32_t)(valid * G * 2));
+  const __amdgpu_buffer_rsrc_t rvs = make_rsrc(vsc + rowbase * G, (uint32_t)(valid * G * 2));
+  const __amdgpu_buffer_rsrc_t rvb = make_rsrc(vbi + rowbase * G, (uint32_t)(valid * G * 2));
+  constexpr uint32_t OOB = 0x80000000u;
+  const bool sact = tid < SI, vact = tid < VI;
+  const int s_key = tid / G, s_g = tid % G;      // K (s, b) item
+  const int v_ko = tid % (TK / 8), v_vd = tid / (TK / 8);  // V item: key octet, 8-dim block
+  const int v_g = 8 * v_vd / GS;
+  uint32_t kw[KIT][UW];
+  uint32_t ksr, kbr;
+  uint32_t vw[8][UW], vsr[8], vbr[8];
+  auto load = [&](int64_t k0) {
+#pragma unroll
+    for (int it = 0; it < KIT; it++) {
+      const int u = tid + NT * it, key = u / (D / 8), c8 = u % (D / 8);
+      const uint32_t off = ((uint32_t)(k0 + key) * KW + (uint32_t)c8 * UW) * 4u;
+      if constexpr (UW == 1) {
+        kw[it][0] = buf_load32(rk, off, 0u);
+      } else {
+        const auto v2 = __builtin_amdgcn_raw_buffer_load_b64(rk, (int)off, 0, 0);
+        kw[it][0] = v2[0];
+        kw[it][1] = v2[1];
+      }
+    }
+    const uint32_t so = sact ? (((uint32_t)(k0 + s_key) * G + (uint32_t)s_g) * 2u) & ~3u : OOB;
+    ksr = __builtin_amdgcn_raw_buffer_load_b32(rks, (int)so, 0, 0);
+    kbr = __builtin_amdgcn_raw_buffer_load_b32(rkb, (int)so, 0, 0);
+#pragma unroll
+    for (int kk = 0; kk < 8; kk++) {
+      const uint32_t key = (uint32_t)(k0 + 8 * v_ko + kk);
+      const uint32_t off = vact ? (key * KW + (uint32_t)v_vd * UW) * 4u : OOB;
+      if constexpr (UW == 1) {
+        vw[kk][0] = buf_load32(rv, off, 0u);
+      } else {
+        const auto v2 = __builtin_amdgcn_raw_buffer_load_b64(rv, (int)off, 0, 0);
+        vw[kk][0] = v2[0];
+        vw[kk][1] = v2[1];
+      }
+      const uint32_t vso = vact ? ((key * (uint32_t)G + (uint32_t)v_g) * 2u) & ~3u : OOB;
+      vsr[kk] = __builtin_amdgcn_raw_buffer_load_b32(rvs, (int)vso, 0, 0);
+      vbr[kk] = __builtin_amdgcn_raw_buffer_load_b32(rvb, (int)vso, 0, 0);
+    }
+  };
+  auto stash = [&](int64_t k0, int buf) {
+#pragma unroll
+    for (int it = 0; it < KIT; it++) {
+      const int u = tid + NT * it, key = u / (D / 8), c8 = u % (D / 8);
+      u32x4_t op;
+      if constexpr (BITS == 4)
+        op = CO::operand(kw[it][0]);
+      else
+        op = CO::operand(kw[it][0], kw[it][1]);
+      *reinterpret_cast<u32x4_t*>(&kt_lds[buf][key * KP + 8 * c8]) = op;
+    }
+    if (sact) {
+      const int sh = 16 * (int)((((uint32_t)(k0 + s_key) * G + (uint32_t)s_g)) & 1u);
+      const float sc = Conv<T>::from_bits((ksr >> sh) & 0xffffu), bi = Conv<T>::from_bits((kbr >> sh) & 0xffffu);
+      ksb[buf][0][s_g][s_key] = sc;
+      ksb[buf][1][s_g][s_key] = __builtin_fmaf(-OFF, sc, bi);
+    }
+    if (vact) {
+      float sc[8], bi[8];
+#pragma unroll
+      for (int kk = 0; kk < 8; kk++) {
+        const int sh = 16 * (int)((((uint32_t)(k0 + 8 * v_ko + kk) * G + (uint32_t)v_g)) & 1u);
+        sc[kk] = Conv<T>::from_bits((vsr[kk] >> sh) & 0xffffu);
+        bi[kk] = Conv<T>::from_bits((vbr[kk] >> sh) & 0xffffu);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        float x[8];
+#pragma unroll
+        for (int kk = 0; kk < 8; kk++) {
+          const uint32_t wv = vw[kk][e * BITS / 32];
+          x[kk] = __builtin_fmaf(sc[kk], (float)((wv >> ((e * BITS) % 32)) & CMASK), bi[kk]);
+        }
+        *reinterpret_cast<u32x4_t*>(&vt_lds[buf][(8 * v_vd + e) * VP + 8 * v_ko]) =
+            u32x4_t{Mma<T>::pack2(x[0], x[1]), Mma<T>::pack2(x[2], x[3]), Mma<T>::pack2(x[4], x[5]),
+                    Mma<T>::pack2(x[6], x[7])};
+      }
+    }
+  };
+
+  f32x4_t oacc[DC];
+#pragma unroll
+  for (int c = 0; c < DC; c++) oacc[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float m_run[4], l_run[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    m_run[i] = -INFINITY;
+    l_run[i] = 0.f;
+  }
+
+  if (kbeg < kend) {
+    load(kbeg);
+    stash(kbeg, 0);
+    if (kbeg + TK < kend) load(kbeg + TK);
+  }
+  lds_barrier();
+  int buf = 0;
+  for (int64_t k0 = kbeg; k0 < kend; k0 += TK) {
+    // ---- scores: two 16-key column tiles, one group at a time -------------
+    f32x4_t sacc[2];
+#pragma unroll
+    for (int ct = 0; ct < 2; ct++) {
+      sacc[ct] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int g = 0; g < G; g++) {
+        f32x4_t part = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < KST; s++) {
+          const u32x4_t bop =
+              *reinterpret_cast<const u32x4_t*>(&kt_lds[buf][(16 * ct + ln) * KP + g * GS + lq * CPQ + 8 * s]);
+          part = Mma<T>::mma(qop[g][s], bop, part);
+        }
+        const float sk = ksb[buf][0][g][16 * ct + ln], bk = ksb[buf][1][g][16 * ct + ln];
+        const float4 xv = *reinterpret_cast<const float4*>(&xw[wave][g][4 * lq]);
+        const float xa[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) sacc[ct][i] = __builtin_fmaf(sk, part[i], __builtin_fmaf(bk, xa[i], sacc[ct][i]));
+      }
+    }
+    if (k0 + TK < kend) stash(k0 + TK, buf ^ 1);
+    if (k0 + 2 * TK < kend) load(k0 + 2 * TK);
+    // ---- online softmax over this tile's 32 keys ---------------------------
+    const bool need_mask = k0 + TK > valid || (causal && k0 + TK - 1 > wpos_lo) ||
+                           (window > 0 && k0 <= wpos_hi - window);
+    float alpha[4], msub[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+#pragma unroll
+      for (int ct = 0; ct < 2; ct++) {
+        if (need_mask) {  // wave-uniform
+          const int64_t j = k0 + 16 * ct + ln;
+          const bool ok = j < valid && (!causal || j <= pos[i]) && (window <= 0 || pos[i] < j + window) && rok[i];
+          sacc[ct][i] = ok ? sacc[ct][i] : -INFINITY;
+        }
+      }
+      float mv = fmaxf(sacc[0][i], sacc[1][i]);
+      mv = fmaxf(mv, __shfl_xor(mv, 1));
+      mv = fmaxf(mv, __shfl_xor(mv, 2));
+      mv = fmaxf(mv, __shfl_xor(mv, 4));
+      mv = fmaxf(mv, __shfl_xor(mv, 8));
+      const float m_old = m_run[i];
+      const float m_new = mv > m_old + 8.0f / LOG2E ? mv : m_old;  // lazy: p <= 2^8
+      alpha[i] = m_new == m_old ? 1.0f : __builtin_amdgcn_exp2f((m_old - m_new) * LOG2E);
+      msub[i] = m_new == -INFINITY ? 0.0f : -m_new * LOG2E;
+      m_run[i] = m_new;
+    }
+    float psum[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      psum[i] = 0.f;
+#pragma unroll
+      for (int ct = 0; ct < 2; ct++) {
+        const uint32_t pb = Conv<T>::to_bits(__builtin_amdgcn_exp2f(__builtin_fmaf(sacc[ct][i], LOG2E, msub[i])));
+        pw[wave][(4 * lq + i) * VP + 16 * ct + ln] = (uint16_t)pb;
+        psum[i] += Conv<T>::from_bits(pb);  // the P the MFMA sees
+      }
+      l_run[i] = l_run[i] * alpha[i] + psum[i];
+    }
+    if (__any(alpha[0] != 1.0f || alpha[1] != 1.0f || alpha[2] != 1.0f || alpha[3] != 1.0f)) {
+#pragma unroll
+      for (int c = 0; c < DC; c++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) oacc[c][i] *= alpha[i];
+    }
+    // ---- O += P V: one 32-key k-step per 16-dim column tile ---------------
+    const u32x4_t pa = *reinterpret_cast<const u32x4_t*>(&pw[wave][ln * VP + 8 * lq]);
+#pragma unroll
+    for (int c = 0; c < DC; c++) {
+      const u32x4_t bv = *reinterpret_cast<const u32x4_t*>(&vt_lds[buf][(16 * c + ln) * VP + 8 * lq]);
+      oacc[c] = Mma<T>::mma(pa, bv, oacc[c]);
+    }
+    lds_barrier();
+    buf ^= 1;
+  }
+
+  // ---- normalise and store: lane holds dims 16 c + ln of rows 4 lq + i ---
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    float lv = l_run[i];
+    lv += __shfl_xor(lv, 1);
+    lv += __shfl_xor(lv, 2);
+    lv += __shfl_xor(lv, 4);
+    lv += __shfl_xor(lv, 8);
+    const float inv = lv > 0.f ? 1.0f / lv : 0.f;
+    if (rok[i]) {
+      const int r = r0 + 4 * lq + i, qd = r / nrep, hd = r % nrep;
+      uint16_t* orow = out + (((int64_t)b * Hq + (int64_t)kvh * nrep + hd) * Lq + qd) * D;
+#pragma unroll
+      for (int c = 0; c < DC; c++) orow[16 * c + ln] = (uint16_t)Conv<T>::to_bits(oacc[c][i] * inv);
+    }
+  }
+}
+
+template <typename T, int BITS>
+int launch_prefill_wide(int D, int gs, const void* q, int B, int Hq, int Hkv, int Lq, const uint32_t* kp,
+                        const void* ks, const void* kb, const uint32_t* vp, const void* vs, const void* vb,
+                        Geometry geo, int causal, int window, float scale, void* out, hipStream_t s) {
+  const int nrep = Hq / Hkv;
+  const int64_t rows = (int64_t)Lq * nrep;
+#define PREW(DV, GV)                                                                                           \
+  if (D == DV && gs == GV) {                                                                                   \
+    using SH = PrefillWideShape<DV, GV, BITS>;                                                                 \
+    dim3 grid((unsigned)((rows + SH::ROWS - 1) / SH::ROWS), (unsigned)Hkv, (unsigned)B);                       \
+    hipLaunchKernelGGL((sdpa_prefill_wide_kernel<T, BITS, DV, GV>), grid, dim3(SH::NT), 0, s,                  \
+                       (const uint16_t*)q, kp, (const uint16_t*)ks, (const uint16_t*)kb, vp, (const uint16_t*)vs, \
+                       (const uint16_t*)vb, Hq, Hkv, Lq, geo, causal, window, scale, (uint16_t*)out);          \
+    MLXQ_LAUNCHED("sdpa_prefill_wide_kernel");                                                                 \
+    return MLXQ_OK;                                                                                            \
+  }
+  PREW(256, 32) PREW(256, 64) PREW(256, 128) PREW(512, 64) PREW(512, 128)
+#undef PREW
+  return mlxq::fail(MLXQ_ERR_UNSUPPORTED, "prefill: no wide MFMA instance for this head_dim/group_size");
+}
+
 template <typename T, int BITS>
 int launch_prefill(int D, int gs, const void* q, int B, int Hq, int Hkv, int Lq, const uint32_t* kp, const void* ks,
                    const void* kb, const uint32_t* vp, const void* vs, const void* vb, Geometry geo, int causal,
@@ -1710,6 +2043,23 @@ extern "C" int mlxq_quantized_sdpa(const void* q, int dtype, int B, int Hq, int 
                                               v_scales, v_biases, geo, causal, window, scale, out, s)
                      : launch_prefill<F16, 8>(D, group_size, q, B, Hq, Hkv, Lq, k_packed, k_scales, k_biases, v_packed,
                                               v_scales, v_biases, geo, causal, window, scale, out, s);
+  }
+  // head_dim 256 / 512 (one row's K scales as aligned dwords)
+  const bool prefill_wide_ok = Lq > 1 && !ring_offset && mlxq::is_half_dtype(dtype) && (bits == 4 || bits == 8) &&
+                               (D == 256 || (D == 512 && group_size >= 64)) && (uintptr_t)k_scales % 4 == 0 &&
+                               (uintptr_t)k_biases % 4 == 0 && (uintptr_t)v_scales % 4 == 0 &&
+                               (uintptr_t)v_biases % 4 == 0 &&
+                               kv_capacity * (int64_t)D * bits / 8 < ((int64_t)1 << 31);
+  if (prefill_wide_ok) {
+    if (dtype == MLXQ_BFLOAT16)
+      return bits == 4 ? launch_prefill_wide<BF16, 4>(D, group_size, q, B, Hq, Hkv, Lq, k_packed, k_scales, k_biases,
+                                                      v_packed, v_scales, v_biases, geo, causal, window, scale, out, s)
+                       : launch_prefill_wide<BF16, 8>(D, group_size, q, B, Hq, Hkv, Lq, k_packed, k_scales, k_biases,
+                                                      v_packed, v_scales, v_biases, geo, causal, window, scale, out, s);
+    return bits == 4 ? launch_prefill_wide<F16, 4>(D, group_size, q, B, Hq, Hkv, Lq, k_packed, k_scales, k_biases,
+                                                   v_packed, v_scales, v_biases, geo, causal, window, scale, out, s)
+                     : launch_prefill_wide<F16, 8>(D, group_size, q, B, Hq, Hkv, Lq, k_packed, k_scales, k_biases,
+                                                   v_packed, v_scales, v_biases, geo, causal, window, scale, out, s);
   }
   dim3 grid((unsigned)Lq, (unsigned)Hq, (unsigned)B);
   MLXQ_DISPATCH_T(dtype, TT, {

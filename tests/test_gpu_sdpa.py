@@ -133,6 +133,24 @@ def test_decode_wide_ring(O, mlxq_dev):
     check(O, got, q, kq, vq, BF16, 1.0, 64, 4, "wide ring", valid_len=lens, ring_off=ring)
 
 
+@pytest.mark.parametrize("B,Hq,Hkv,L,N,D,gs,bits,dtype,scale,window", [
+    (1, 16, 2, 70, 600, 512, 64, 4, BF16, 1.0, 0),      # Gemma4 full attention: nRep 8, D 512, scale 1
+    (1, 16, 2, 33, 300, 512, 128, 8, F16, 1.0, 0),      # group 128, 8-bit
+    (2, 8, 2, 40, 257, 256, 32, 4, BF16, 0.0625, 0),    # D 256, 8 groups, batch 2
+    (1, 4, 4, 129, 129, 256, 64, 8, BF16, 0.0625, 50),  # prompt (queries = keys) under a window
+    (1, 8, 1, 17, 2000, 512, 64, 4, BF16, 1.0, 0),      # short chunk over a long cache
+])
+def test_prefill_wide(O, mlxq_dev, B, Hq, Hkv, L, N, D, gs, bits, dtype, scale, window):
+    """Chunked prefill at head_dim 256 / 512 (the wide MFMA kernel: 16 rows
+    per wave, exact K operands, V dequantized through LDS), bottom-right
+    causal (+ window), against the fp64 oracle."""
+    from mlxq import ops
+
+    q, kq, vq = case(O, B, Hq, Hkv, L, N, D, gs, bits, dtype, 30 + L)
+    got = run(O, mlxq_dev, q, kq, vq, dtype, scale, gs, bits, mask=ops.createCausalMask(L, N - L, window or None))
+    check(O, got, q, kq, vq, dtype, scale, gs, bits, "prefill wide", causal=True, window=window)
+
+
 def test_decode_empty_rows_are_zero(O, mlxq_dev):
     q, kq, vq = case(O, 3, 8, 2, 1, 64, 128, 64, 4, BF16, 5)
     got = run(O, mlxq_dev, q, kq, vq, BF16, 1.0, 64, 4, valid=[0, 10, 0], ring=[3, 7, 0])
