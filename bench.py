@@ -22,6 +22,9 @@ Also measured in the same run and reported beside it:
                         the largest GEMV)
   prefill_chunk         Lq=2048 new queries over 32768 cached keys (4-bit),
                         Hq=32 Hkv=8 D=128, causal
+  gemma4_full_attention the 26B-A4B full-attention shape (Hq=16, Hkv=2,
+                        D=512, 4-bit): decode at 32k context and a 512-query
+                        causal chunk over 8192 keys
   cpu_baseline          the CPU oracle's decode on the host, bounded sample
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--quick]
@@ -433,6 +436,21 @@ def main():
                                   "TFLOP/s": round(f5 / (md5 * 1e-6) / 1e12, 1),
                                   "pct_mfma_bf16_peak": round(100 * f5 / (md5 * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 1)}
         del k5
+        log("bench: gemma4 full attention (D 512)")
+        g4 = {}
+        lg, bg, kg = decode_workload(B=1, Hq=16, Hkv=2, D=512, N=32768, gs=64, bits=4)
+        msg = timer.graph_step_ms(lg, 100, 10)
+        g4["decode_32k"] = {"us_per_call": round(msg * 1e3, 2), "algorithmic_bytes": bg,
+                            "GB/s": round(bg / (msg * 1e-3) / 1e9, 1),
+                            "pct_hbm_peak": round(100 * bg / (msg * 1e-3) / 1e9 / HBM_PEAK_GBS, 1)}
+        del kg
+        lp, fp, kpw = prefill_workload(Hq=16, Hkv=2, D=512, Lq=512, N=8192)
+        mp, mdp = timer.per_launch_us(lp, 5)
+        g4["prefill_512x8192"] = {"us_per_call": round(mdp, 1), "flops": fp,
+                                  "TFLOP/s": round(fp / (mdp * 1e-6) / 1e12, 1),
+                                  "pct_mfma_bf16_peak": round(100 * fp / (mdp * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 1)}
+        del kpw
+        extra["gemma4_full_attention"] = g4
 
     cpu = None
     if not args.no_cpu:
