@@ -559,23 +559,31 @@ __global__ void __launch_bounds__(512) sdpa_decode_mfma_kernel(
 // Split-K merge: out[b, kvh*nrep + h, d] = sum_c U_c e^{M_c - M} / sum_c L_c e^{M_c - M}
 // over the chunks c of row b (the reference's deterministic flash-decoding
 // merge, src/model/fused-decode-kernel.ts:205-222).  Workgroup (cb, kvh, b)
-// owns 64 float4 columns of (h, d); its four waves fold the chunks
-// c = wave, wave + 4, ... with an online merge and combine in LDS in fixed
-// order.  Rows whose keys fit one chunk were finished by the partial kernel.
+// owns 64 float4 columns of (h, d); its waves (blockDim.x / 64, at most
+// MERGE_WAVES) fold the chunks c = wave, wave + waves, ... with an online
+// merge and combine in LDS in fixed order (16 waves: a 128-chunk row keeps
+// 8 loads in flight per wave instead of walking 32).  chunk > 0: the chunks
+// are the decode chunks of row b (rows whose keys fit one chunk were
+// finished by the partial kernel); chunk == 0: every row has nslots chunks
+// (the split prefill, whose rows h are (head, query) pairs in output order).
+// A chunk with no unmasked key (M = -inf) adds nothing; a row with none
+// at all stores 0, as the single-pass kernels do.
+constexpr int MERGE_WAVES = 16;
 template <typename T>
-__global__ void __launch_bounds__(256) sdpa_decode_merge_kernel(const float4* __restrict__ part_o,
+__global__ void __launch_bounds__(MERGE_WAVES * 64) sdpa_decode_merge_kernel(const float4* __restrict__ part_o,
                                                                 const float2* __restrict__ part_ml, int Hq, int Hkv,
                                                                 int D, Geometry geo, int chunk, int nslots,
                                                                 uint16_t* __restrict__ out) {
-  __shared__ float4 ul[4][64];
-  __shared__ float2 mll[4][64];
+  __shared__ float4 ul[MERGE_WAVES][64];
+  __shared__ float2 mll[MERGE_WAVES][64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nw = (int)(blockDim.x >> 6);
   const int b = blockIdx.z, kvh = blockIdx.y;
   const int nrep = Hq / Hkv;
   const int cols = nrep * D / 4;
   const int col = blockIdx.x * 64 + lane;
-  const int nch = chunk_range(geo, b, chunk, 0).nch;
-  if (nch <= 1) return;
+  const int nch = chunk > 0 ? chunk_range(geo, b, chunk, 0).nch : nslots;
+  if (chunk > 0 && nch <= 1) return;
   const int64_t bk = (int64_t)b * Hkv + kvh;
   const bool active = col < cols;
   const int colc = active ? col : cols - 1;
@@ -585,9 +593,10 @@ __global__ void __launch_bounds__(256) sdpa_decode_merge_kernel(const float4* __
   float M = -INFINITY, L = 0.f;
   float4 U = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll 8
-  for (int cc = wave; cc < nch; cc += 4) {
+  for (int cc = wave; cc < nch; cc += nw) {
     const float2 ml = pml[cc * nrep + h];
     const float4 u = po[(int64_t)cc * cols + colc];
+    if (ml.x == -INFINITY) continue;  // fully masked chunk (its L and U are 0)
     const float Mn = fmaxf(M, ml.x);
     const float a = __builtin_amdgcn_exp2f(M - Mn), f = __builtin_amdgcn_exp2f(ml.x - Mn);  // M = -inf -> a = 0
     L = L * a + ml.y * f;
@@ -602,13 +611,12 @@ __global__ void __launch_bounds__(256) sdpa_decode_merge_kernel(const float4* __
   lds_barrier();
   if (wave != 0 || !active) return;
   float Mt = -INFINITY;
-#pragma unroll
-  for (int w = 0; w < 4; w++) Mt = fmaxf(Mt, mll[w][lane].x);
+  for (int w = 0; w < nw; w++) Mt = fmaxf(Mt, mll[w][lane].x);
   float Lt = 0.f;
   float4 Ut = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-  for (int w = 0; w < 4; w++) {
-    const float f = __builtin_amdgcn_exp2f(mll[w][lane].x - Mt);  // wave with no chunk: -inf -> 0
+  for (int w = 0; w < nw; w++) {
+    const float mw = mll[w][lane].x;
+    const float f = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - Mt);  // wave with no chunk adds 0
     const float4 u = ul[w][lane];
     Lt = __builtin_fmaf(f, mll[w][lane].y, Lt);
     Ut.x = __builtin_fmaf(f, u.x, Ut.x);
@@ -616,11 +624,12 @@ __global__ void __launch_bounds__(256) sdpa_decode_merge_kernel(const float4* __
     Ut.z = __builtin_fmaf(f, u.z, Ut.z);
     Ut.w = __builtin_fmaf(f, u.w, Ut.w);
   }
+  const bool any = Lt > 0.f;
   const int64_t o = ((int64_t)b * Hq + (int64_t)kvh * nrep) * D + (int64_t)col * 4;
-  Conv<T>::store(out, o, Ut.x / Lt);
-  Conv<T>::store(out, o + 1, Ut.y / Lt);
-  Conv<T>::store(out, o + 2, Ut.z / Lt);
-  Conv<T>::store(out, o + 3, Ut.w / Lt);
+  Conv<T>::store(out, o, any ? Ut.x / Lt : 0.f);
+  Conv<T>::store(out, o + 1, any ? Ut.y / Lt : 0.f);
+  Conv<T>::store(out, o + 2, any ? Ut.z / Lt : 0.f);
+  Conv<T>::store(out, o + 3, any ? Ut.w / Lt : 0.f);
 }
 
 // ===================================================== MFMA decode, wide rows
@@ -633,36 +642,67 @@ __global__ void __launch_bounds__(256) sdpa_decode_merge_kernel(const float4* __
 // streamed in 128-key tiles:
 //   * scores S = Q K^T on v_mfma_f32_16x16x32 with the heads as rows (A = q',
 //     loaded once) and 16 keys per wave as columns (B = exact code operands
-//     OFF + c straight from memory; lane quarter lq holds codes
-//     [lq gs/4, (lq+1) gs/4) of every group, so a k-step never leaves a
-//     group); per group S += s_k * D + (b_k - OFF s_k) * X_g, s_k and b_k
-//     being per-lane scalars (the column is the key) and X_g the head's sum
-//     of q' over the group -- no rounding of the dequantized K;
+//     OFF + c straight from memory).  Each K load reads 16 keys x 64
+//     contiguous bytes (lane quarter lq: bytes [16 lq, 16 lq + 16) of the
+//     64); a 4 x 4 dword transpose across the quarters (v_permlane32_swap,
+//     v_permlane16_swap) then gives every k-step 32 consecutive codes, so
+//     a k-step never leaves a group.  Per group S += s_k * D +
+//     (b_k - OFF s_k) * X_g, s_k and b_k being per-lane scalars (the
+//     column is the key) and X_g the head's sum of q' over the group -- no
+//     rounding of the dequantized K;
 //   * one tile max per head shared through LDS, P = exp2(S - m) written to
 //     LDS as T, the row sum taken over the same T values;
 //   * V dequantized once per tile (fp32 s * c + b -> T) into a transposed
 //     LDS tile, and O += P V with each wave owning D/8 output dims (no
-//     cross-wave output merge);
+//     cross-wave output merge).  A staging item is one 16-byte block of 4
+//     consecutive keys, so each V load instruction reads whole rows;
+//     smaller loads spread over many rows cost more in request count
+//     than in bytes (the memory pipeline, not HBM, was the limit);
 //   * the next tile's codes and scales are requested once this one's are
 //     consumed (after the score MFMAs), ahead of its softmax and P V.
 // Chunks write (U, M, L) partials for sdpa_decode_merge_kernel, exactly as
 // the kernel above does.
 template <int D, int GS, int BITS>
 struct WideShape {
-  static constexpr int NW = 8, TK = 128;          // waves, keys per tile (16 per wave)
+  static constexpr int NW = 8;                    // waves (4 waves of 64-key tiles measured slower)
+  static constexpr int TK = 16 * NW;              // keys per tile (16 per wave)
   static constexpr int G = D / GS;
-  static constexpr int KW = D * BITS / 32;        // code words per cache row
-  static constexpr int CPQ = GS / 4;              // codes per lane quarter per group
-  static constexpr int WPQ = CPQ * BITS / 32;     // ... as words
-  static constexpr int KST = GS / 32;             // 16x16x32 k-steps per group
+  static constexpr int RB = D * BITS / 8;         // bytes per cache row
+  static constexpr int KW = RB / 4;               // code words per cache row
+  static constexpr int KI = RB / 64;              // K loads per lane: 16 keys x 64 bytes each
+  static constexpr int NKS = D / 32;              // 16x16x32 k-steps per row
+  static constexpr int KST = GS / 32;             // ... per group
   static constexpr int VTP = TK + 8;              // V^T / P row pitch (T elements)
   static constexpr int DPW = D / NW;              // output dims per wave
   static constexpr int CT = DPW / 16;             // 16-dim output column tiles per wave
-  static constexpr int NVI = (TK / 8) * (D / 16); // V staging items (8 keys x 16 dims)
-  static constexpr int VWK = 16 * BITS / 32;      // code words per key of an item
+  static constexpr int NDB = RB / 16;             // 16-byte blocks per row
+  static constexpr int DB = 128 / BITS;           // dims per block
+  static constexpr int NVI = (TK / 4) * NDB;      // V staging items (4 keys x one block)
+  static constexpr int IPT = (NVI + NW * 64 - 1) / (NW * 64);
   static constexpr int GW = (G + 1) / 2;          // dwords per row of G scales
   static constexpr int MAXC = 1024;
 };
+
+// V^T column swizzle: the 8-key block cb of dim row d is stored at block
+// cb ^ ((d / DB) % NB), NB = keys per tile / 8, so the lanes of one staging
+// store (same dim of consecutive 16-byte blocks) spread over the LDS banks.
+template <int DB, int NB>
+__device__ __forceinline__ int vt_block(int d, int cb) {
+  return cb ^ ((d / DB) & (NB - 1));
+}
+
+// 4 x 4 dword transpose across the lane quarters (lanes l, l+16, l+32, l+48):
+// on entry quarter q holds a_q[0..3]; on exit word k of quarter q is a_k[q].
+__device__ __forceinline__ void quarter_transpose(uint32_t (&w)[4]) {
+  auto s02 = __builtin_amdgcn_permlane32_swap(w[0], w[2], false, false);
+  auto s13 = __builtin_amdgcn_permlane32_swap(w[1], w[3], false, false);
+  auto s01 = __builtin_amdgcn_permlane16_swap(s02[0], s13[0], false, false);
+  auto s23 = __builtin_amdgcn_permlane16_swap(s02[1], s13[1], false, false);
+  w[0] = s01[0];
+  w[1] = s01[1];
+  w[2] = s23[0];
+  w[3] = s23[1];
+}
 
 template <typename T, int BITS, int D, int GS>
 __global__ void __launch_bounds__(512) sdpa_decode_wide_kernel(
@@ -672,11 +712,13 @@ __global__ void __launch_bounds__(512) sdpa_decode_wide_kernel(
     uint16_t* __restrict__ out, float* __restrict__ part_o, float2* __restrict__ part_ml) {
   using SH = WideShape<D, GS, BITS>;
   using CO = CodeOps<T, BITS>;
-  constexpr int NW = SH::NW, TK = SH::TK, G = SH::G, KW = SH::KW, CPQ = SH::CPQ, WPQ = SH::WPQ, KST = SH::KST;
-  constexpr int VTP = SH::VTP, DPW = SH::DPW, CT = SH::CT, NVI = SH::NVI, VWK = SH::VWK, GW = SH::GW;
+  constexpr int NW = SH::NW, TK = SH::TK, G = SH::G, KW = SH::KW, KI = SH::KI, NKS = SH::NKS, KST = SH::KST;
+  constexpr int VTP = SH::VTP, DPW = SH::DPW, CT = SH::CT, NDB = SH::NDB, DB = SH::DB, NVI = SH::NVI;
+  constexpr int IPT = SH::IPT, GW = SH::GW;
   constexpr float OFF = CO::OFFSET;
   constexpr uint32_t CMASK = (1u << BITS) - 1u;
-  static_assert(G <= 8 && CT >= 1 && NVI <= NW * 64, "wide decode geometry");
+  constexpr int NB = TK / 8;
+  static_assert(G <= 8 && CT >= 1 && KI >= 1 && TK % 32 == 0, "wide decode geometry");
   __shared__ __align__(16) uint16_t vt[D * VTP];  // V^T tile, T
   __shared__ __align__(16) uint16_t pl[16 * VTP]; // P tile [head][key], T
   __shared__ float xsum[G][16];                   // X[group][head]
@@ -699,32 +741,6 @@ __global__ void __launch_bounds__(512) sdpa_decode_wide_kernel(
   const int nk = cr.nk;
   const int ntiles = (nk + TK - 1) / TK;
 
-  // ---- q' (A operand: row = head ln, k slots of quarter lq) and X ----------
-  const float scale_t = Conv<T>::round(scale);
-  const bool apply_scale = scale != 1.0f;
-  const bool hok = ln < nrep;
-  const uint16_t* qrow = q + out_base + (int64_t)(hok ? ln : 0) * D;
-  u32x4_t qop[G][KST];
-#pragma unroll
-  for (int g = 0; g < G; g++) {
-    float xp = 0.f;
-#pragma unroll
-    for (int s = 0; s < KST; s++) {
-      u32x4_t raw = hok ? *reinterpret_cast<const u32x4_t*>(qrow + g * GS + lq * CPQ + 8 * s) : u32x4_t{0u, 0u, 0u, 0u};
-#pragma unroll
-      for (int p2 = 0; p2 < 4; p2++) {
-        const float lo = scaled_q<T>(Conv<T>::from_bits(raw[p2] & 0xffffu), scale_t, apply_scale);
-        const float hi = scaled_q<T>(Conv<T>::from_bits(raw[p2] >> 16), scale_t, apply_scale);
-        raw[p2] = Mma<T>::pack2(lo, hi);
-        xp += lo + hi;
-      }
-      qop[g][s] = permute8<CO::ORDER>(raw);
-    }
-    xp += __shfl_xor(xp, 16);
-    xp += __shfl_xor(xp, 32);
-    if (wave == 0 && lq == 0) xsum[g][ln] = xp;
-  }
-
   // ---- descriptors (keys past the chunk read 0) ----------------------------
   const int64_t row0 = ((int64_t)b * Hkv + kvh) * geo.cap + cr.slot0;
   const uint32_t nk32 = (uint32_t)nk;
@@ -735,89 +751,148 @@ __global__ void __launch_bounds__(512) sdpa_decode_wide_kernel(
   const __amdgpu_buffer_rsrc_t rvs = make_rsrc(vsc + row0 * G, nk32 * (uint32_t)(2 * G));
   const __amdgpu_buffer_rsrc_t rvb = make_rsrc(vbi + row0 * G, nk32 * (uint32_t)(2 * G));
 
-  // K side of a tile: lane (key ln of this wave's 16, quarter lq)
+  // K side of a tile: lane (key ln of this wave's 16, quarter lq); w[j] is
+  // bytes [64 j + 16 lq, 64 j + 16 lq + 16) of the row until transposed
   struct KSlot {
-    uint32_t w[G][WPQ];
+    uint32_t w[KI][4];
     uint32_t s[GW], bb[GW];
   };
-  // V side: item it = tid (key octet it % 16 fastest, 16-dim block it / 16)
+  // V side: item it = tid + 512 p is 16-byte block it % NDB of keys
+  // 4 (it / NDB) + [0, 4); s / bb hold each key's dword with the block's group
   struct VSlot {
-    uint32_t w[8][VWK];
-    uint32_t s[8], bb[8];  // the dword holding each key's scale / bias of the block's group
+    uint32_t w[IPT][4][4];
+    uint32_t s[IPT][4], bb[IPT][4];
   };
-  const bool vact = tid < NVI;
-  const int ko = tid % 16, db = tid / 16;
-  const int vg = (16 * db) / GS;
   auto load_k = [&](int t, KSlot& k) {
     const uint32_t key = (uint32_t)(TK * t + 16 * wave + ln);
 #pragma unroll
-    for (int g = 0; g < G; g++) {
-      const uint32_t off = (key * KW + (uint32_t)g * (GS * BITS / 32) + (uint32_t)lq * WPQ) * 4u;
-      if constexpr (WPQ == 1) {
-        k.w[g][0] = buf_load32(rk, off, 0u);
-      } else if constexpr (WPQ == 2) {
-        const auto v = __builtin_amdgcn_raw_buffer_load_b64(rk, (int)off, 0, 0);
-        k.w[g][0] = v[0];
-        k.w[g][1] = v[1];
-      } else {
-#pragma unroll
-        for (int h = 0; h < WPQ / 4; h++) {
-          const u32x4_t v = buf_load128(rk, off + 16u * h, 0u);
-          k.w[g][4 * h] = v.x;
-          k.w[g][4 * h + 1] = v.y;
-          k.w[g][4 * h + 2] = v.z;
-          k.w[g][4 * h + 3] = v.w;
-        }
-      }
+    for (int j = 0; j < KI; j++) {
+      const u32x4_t v = buf_load128(rk, (key * KW + 16u * j + 4u * lq) * 4u, 0u);
+      k.w[j][0] = v.x;
+      k.w[j][1] = v.y;
+      k.w[j][2] = v.z;
+      k.w[j][3] = v.w;
     }
     load_row_groups_buf<G>(rks, key * (uint32_t)(2 * G), 0u, k.s);
     load_row_groups_buf<G>(rkb, key * (uint32_t)(2 * G), 0u, k.bb);
   };
   auto load_v = [&](int t, VSlot& v) {
 #pragma unroll
-    for (int kk = 0; kk < 8; kk++) {
-      const uint32_t key = (uint32_t)(TK * t + 8 * ko + kk);
-      const uint32_t off = vact ? (key * KW + (uint32_t)db * VWK) * 4u : 0x80000000u;  // inactive: reads 0
-      if constexpr (VWK == 2) {
-        const auto x = __builtin_amdgcn_raw_buffer_load_b64(rv, (int)off, 0, 0);
-        v.w[kk][0] = x[0];
-        v.w[kk][1] = x[1];
-      } else {
+    for (int p = 0; p < IPT; p++) {
+      const int it = tid + NW * 64 * p;
+      const bool act = it < NVI;
+      const int db = it % NDB, kq = it / NDB;
+      const int vg = (DB * db) / GS;
+#pragma unroll
+      for (int kk = 0; kk < 4; kk++) {
+        const uint32_t key = (uint32_t)(TK * t + 4 * kq + kk);
+        const uint32_t off = act ? (key * KW + 4u * db) * 4u : 0x80000000u;  // inactive: reads 0
         const u32x4_t x = buf_load128(rv, off, 0u);
-        v.w[kk][0] = x.x;
-        v.w[kk][1] = x.y;
-        v.w[kk][2] = x.z;
-        v.w[kk][3] = x.w;
+        v.w[p][kk][0] = x.x;
+        v.w[p][kk][1] = x.y;
+        v.w[p][kk][2] = x.z;
+        v.w[p][kk][3] = x.w;
+        const uint32_t so = act ? ((key * (uint32_t)G + (uint32_t)vg) * 2u) & ~3u : 0x80000000u;
+        v.s[p][kk] = __builtin_amdgcn_raw_buffer_load_b32(rvs, (int)so, 0, 0);
+        v.bb[p][kk] = __builtin_amdgcn_raw_buffer_load_b32(rvb, (int)so, 0, 0);
       }
-      const uint32_t so = vact ? ((key * (uint32_t)G + (uint32_t)vg) * 2u) & ~3u : 0x80000000u;
-      v.s[kk] = __builtin_amdgcn_raw_buffer_load_b32(rvs, (int)so, 0, 0);
-      v.bb[kk] = __builtin_amdgcn_raw_buffer_load_b32(rvb, (int)so, 0, 0);
     }
   };
-  // V: s * c + b -> T, written as V^T rows (16 dims) of 8 keys
+  // V: s * c + b -> T, written as V^T rows (one per dim) of 4 keys, the key
+  // blocks swizzled by vt_block
   auto stage_v = [&](int t, const VSlot& v) {
-    if (!vact) return;
-    const int sh = 16 * (int)((((uint32_t)(TK * t + 8 * ko) * (uint32_t)G + (uint32_t)vg)) & 1u);
-    float sc[8], bi[8];
 #pragma unroll
-    for (int kk = 0; kk < 8; kk++) {  // G * key + vg has the parity of vg for even G
-      const int shk = (G % 2 == 0) ? sh : 16 * (int)((((uint32_t)(TK * t + 8 * ko + kk) * (uint32_t)G + (uint32_t)vg)) & 1u);
-      sc[kk] = Conv<T>::from_bits((v.s[kk] >> shk) & 0xffffu);
-      bi[kk] = Conv<T>::from_bits((v.bb[kk] >> shk) & 0xffffu);
-    }
+    for (int p = 0; p < IPT; p++) {
+      const int it = tid + NW * 64 * p;
+      if (it >= NVI) continue;
+      const int db = it % NDB, kq = it / NDB;
+      const int vg = (DB * db) / GS;
+      float sc[4], bi[4];
 #pragma unroll
-    for (int e = 0; e < 16; e++) {
-      float x[8];
-#pragma unroll
-      for (int kk = 0; kk < 8; kk++) {
-        const uint32_t wv = v.w[kk][e * BITS / 32];
-        x[kk] = __builtin_fmaf(sc[kk], (float)((wv >> ((e * BITS) % 32)) & CMASK), bi[kk]);
+      for (int kk = 0; kk < 4; kk++) {
+        const int shk = 16 * (int)((((uint32_t)(TK * t + 4 * kq + kk) * (uint32_t)G + (uint32_t)vg)) & 1u);
+        sc[kk] = Conv<T>::from_bits((v.s[p][kk] >> shk) & 0xffffu);
+        bi[kk] = Conv<T>::from_bits((v.bb[p][kk] >> shk) & 0xffffu);
       }
-      *reinterpret_cast<u32x4_t*>(&vt[(16 * db + e) * VTP + 8 * ko]) =
-          u32x4_t{Mma<T>::pack2(x[0], x[1]), Mma<T>::pack2(x[2], x[3]), Mma<T>::pack2(x[4], x[5]),
-                  Mma<T>::pack2(x[6], x[7])};
+      const int col = 8 * vt_block<DB, NB>(DB * db, kq >> 1) + 4 * (kq & 1);  // every dim of the block: same swizzle
+#pragma unroll
+      for (int e = 0; e < DB; e++) {
+        float x[4];
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) {
+          const uint32_t wv = v.w[p][kk][e * BITS / 32];
+          x[kk] = __builtin_fmaf(sc[kk], (float)((wv >> ((e * BITS) % 32)) & CMASK), bi[kk]);
+        }
+        *reinterpret_cast<uint2*>(&vt[(DB * db + e) * VTP + col]) =
+            make_uint2(Mma<T>::pack2(x[0], x[1]), Mma<T>::pack2(x[2], x[3]));
+      }
     }
   };
+
+  // ---- q' (A operand) and X ------------------------------------------------
+  // The nrep query rows are read once per workgroup (16 bytes a thread),
+  // scaled, and staged in LDS (the V^T tile, free until the first tile is
+  // staged); tile 0's code loads are issued in between so their latency
+  // overlaps.  A-operand row = head ln; k-step ks covers dims
+  // [32 ks, 32 ks + 32), quarter lq the dims its transposed K words carry:
+  // 4-bit 32 ks + 8 lq + [0, 8), 8-bit 32 ks + 4 lq + [0, 4) then
+  // 32 ks + 16 + 4 lq + [0, 4).
+  constexpr int QP = D + 8;  // staged q' row pitch (T elements)
+  constexpr int QIT = (16 * (D / 8) + NW * 64 - 1) / (NW * 64);
+  static_assert(16 * QP <= D * VTP, "q' staging fits in the V^T tile");
+  const int qitems = nrep * (D / 8);
+  u32x4_t qraw[QIT];
+#pragma unroll
+  for (int p = 0; p < QIT; p++) {
+    const int it = tid + NW * 64 * p;
+    qraw[p] = it < qitems ? *reinterpret_cast<const u32x4_t*>(q + out_base + 8 * (int64_t)it) : u32x4_t{0u, 0u, 0u, 0u};
+  }
+  KSlot kslot;
+  VSlot vslot;
+  load_k(0, kslot);
+  load_v(0, vslot);
+  const float scale_t = Conv<T>::round(scale);
+  const bool apply_scale = scale != 1.0f;
+#pragma unroll
+  for (int p = 0; p < QIT; p++) {
+    const int it = tid + NW * 64 * p;
+    if (it < qitems) {
+      u32x4_t r = qraw[p];
+#pragma unroll
+      for (int p2 = 0; p2 < 4; p2++)
+        r[p2] = Mma<T>::pack2(scaled_q<T>(Conv<T>::from_bits(r[p2] & 0xffffu), scale_t, apply_scale),
+                              scaled_q<T>(Conv<T>::from_bits(r[p2] >> 16), scale_t, apply_scale));
+      *reinterpret_cast<u32x4_t*>(&vt[(it / (D / 8)) * QP + 8 * (it % (D / 8))]) = r;
+    }
+  }
+  lds_barrier();  // q' in
+  const bool hok = ln < nrep;
+  const uint16_t* qrow = vt + ln * QP;
+  u32x4_t qop[NKS];
+#pragma unroll
+  for (int g = 0; g < G; g++) {
+    float xp = 0.f;
+#pragma unroll
+    for (int s = 0; s < KST; s++) {
+      const int ks = g * KST + s;
+      u32x4_t raw = {0u, 0u, 0u, 0u};
+      if (hok) {
+        if constexpr (BITS == 4) {
+          raw = *reinterpret_cast<const u32x4_t*>(qrow + 32 * ks + 8 * lq);
+        } else {
+          const uint2 lo = *reinterpret_cast<const uint2*>(qrow + 32 * ks + 4 * lq);
+          const uint2 hi = *reinterpret_cast<const uint2*>(qrow + 32 * ks + 16 + 4 * lq);
+          raw = u32x4_t{lo.x, lo.y, hi.x, hi.y};
+        }
+      }
+#pragma unroll
+      for (int p2 = 0; p2 < 4; p2++) xp += Conv<T>::from_bits(raw[p2] & 0xffffu) + Conv<T>::from_bits(raw[p2] >> 16);
+      qop[ks] = permute8<CO::ORDER>(raw);
+    }
+    xp += __shfl_xor(xp, 16);
+    xp += __shfl_xor(xp, 32);
+    if (wave == 0 && lq == 0) xsum[g][ln] = xp;
+  }
 
   // ---- online softmax state: rows 4 lq + i (heads) of the 16x16 layouts ----
   float m_run[4], l_run[4];
@@ -835,6 +910,8 @@ __global__ void __launch_bounds__(512) sdpa_decode_wide_kernel(
   // MFMAs) before the next tile's loads refill the same slots
   auto tile = [&](int t, KSlot& k, VSlot& v) {
     stage_v(t, v);
+#pragma unroll
+    for (int j = 0; j < KI; j++) quarter_transpose(k.w[j]);
     // scores of this wave's 16 keys, log2 units
     f32x4_t sacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -842,12 +919,13 @@ __global__ void __launch_bounds__(512) sdpa_decode_wide_kernel(
       f32x4_t part = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < KST; s++) {
+        const int ks = g * KST + s;
         u32x4_t bop;
         if constexpr (BITS == 4)
-          bop = CodeOps<T, 4>::operand(k.w[g][s], magic);
+          bop = CodeOps<T, 4>::operand(k.w[ks / 4][ks % 4], magic);
         else
-          bop = CodeOps<T, BITS>::operand(k.w[g][2 * s], k.w[g][2 * s + 1]);
-        part = Mma<T>::mma(qop[g][s], bop, part);
+          bop = CodeOps<T, BITS>::operand(k.w[ks / 2][2 * (ks % 2)], k.w[ks / 2][2 * (ks % 2) + 1]);
+        part = Mma<T>::mma(qop[ks], bop, part);
       }
       const float ks = Conv<T>::from_bits(group_bits<G>(k.s, g));
       const float kd = (Conv<T>::from_bits(group_bits<G>(k.bb, g)) - OFF * ks) * LOG2E;
@@ -904,18 +982,15 @@ __global__ void __launch_bounds__(512) sdpa_decode_wide_kernel(
       const u32x4_t a = *reinterpret_cast<const u32x4_t*>(&pl[ln * VTP + 32 * kq + 8 * lq]);
 #pragma unroll
       for (int ct = 0; ct < CT; ct++) {
-        const u32x4_t bv = *reinterpret_cast<const u32x4_t*>(&vt[(DPW * wave + 16 * ct + ln) * VTP + 32 * kq + 8 * lq]);
+        const int d = DPW * wave + 16 * ct + ln;
+        const u32x4_t bv = *reinterpret_cast<const u32x4_t*>(&vt[d * VTP + 8 * vt_block<DB, NB>(d, 4 * kq + lq)]);
         oacc[ct] = Mma<T>::mma(a, bv, oacc[ct]);
       }
     }
     lds_barrier();  // the tile's V^T and P are free again
   };
 
-  KSlot kslot;
-  VSlot vslot;
-  load_k(0, kslot);
-  load_v(0, vslot);
-  lds_barrier();  // X in
+  lds_barrier();  // X in; q' reads done before V^T staging
   for (int t = 0; t < ntiles; t++) tile(t, kslot, vslot);
 
   // ---- row sums over keys (lanes) and waves; store -------------------------
@@ -1402,7 +1477,7 @@ __global__ void __launch_bounds__(256) sdpa_prefill_wide_kernel(
     const uint16_t* __restrict__ q, const uint32_t* __restrict__ kp, const uint16_t* __restrict__ ksc,
     const uint16_t* __restrict__ kbi, const uint32_t* __restrict__ vp, const uint16_t* __restrict__ vsc,
     const uint16_t* __restrict__ vbi, int Hq, int Hkv, int Lq, Geometry geo, int causal, int window, float scale,
-    uint16_t* __restrict__ out) {
+    uint16_t* __restrict__ out, int nsplit, float* __restrict__ part_o, float2* __restrict__ part_ml) {
   using SH = PrefillWideShape<D, GS, BITS>;
   using CO = CodeOps<T, BITS>;
   constexpr int NW = SH::NW, ROWS = SH::ROWS, NT = SH::NT, TK = SH::TK, G = SH::G, KW = SH::KW, CPQ = SH::CPQ;
@@ -1426,8 +1501,10 @@ __global__ void __launch_bounds__(256) sdpa_prefill_wide_kernel(
   const int64_t rowbase = ((int64_t)b * Hkv + kvh) * geo.cap;
 
   // ---- rows: r = query * nrep + head; the A operand's row is ln, the
-  // accumulator rows are 4 lq + i --------------------------------------------
-  const int r0 = blockIdx.x * ROWS + 16 * wave;
+  // accumulator rows are 4 lq + i.  blockIdx.x = row block * nsplit + key
+  // split ---------------------------------------------------------------------
+  const int rb = (int)blockIdx.x / nsplit, sp = (int)blockIdx.x % nsplit;
+  const int r0 = rb * ROWS + 16 * wave;
   int64_t pos[4];
   bool rok[4];
 #pragma unroll
@@ -1436,12 +1513,19 @@ __global__ void __launch_bounds__(256) sdpa_prefill_wide_kernel(
     rok[i] = qi < Lq;
     pos[i] = valid - Lq + (rok[i] ? qi : Lq - 1);
   }
-  const int qi_lo = blockIdx.x * ROWS / nrep;
-  const int qi_hi = min(Lq - 1, (blockIdx.x * ROWS + ROWS - 1) / nrep);
+  const int qi_lo = rb * ROWS / nrep;
+  const int qi_hi = min(Lq - 1, (rb * ROWS + ROWS - 1) / nrep);
   int64_t kend = valid, kbeg = 0;
   if (causal) kend = min(kend, valid - Lq + qi_hi + 1);
   if (window > 0) kbeg = max((int64_t)0, valid - Lq + qi_lo - window + 1);
   kbeg = kbeg / TK * TK;
+  if (nsplit > 1) {  // this split's whole tiles of the row block's key range (maybe none)
+    const int64_t ntk = kend > kbeg ? (kend - kbeg + TK - 1) / TK : 0;
+    const int64_t per = (ntk + nsplit - 1) / nsplit;
+    const int64_t s0 = kbeg + (int64_t)sp * per * TK;
+    kend = min(kend, s0 + per * TK);
+    kbeg = s0;
+  }
   const int wq_lo = min(Lq - 1, r0 / nrep), wq_hi = min(Lq - 1, (r0 + 15) / nrep);
   const int64_t wpos_lo = valid - Lq + wq_lo, wpos_hi = valid - Lq + wq_hi;
 
@@ -1667,9 +1751,16 @@ __global__ void __launch_bounds__(256) sdpa_prefill_wide_kernel(
     const float inv = lv > 0.f ? 1.0f / lv : 0.f;
     if (rok[i]) {
       const int r = r0 + 4 * lq + i, qd = r / nrep, hd = r % nrep;
-      uint16_t* orow = out + (((int64_t)b * Hq + (int64_t)kvh * nrep + hd) * Lq + qd) * D;
+      if (nsplit == 1) {
+        uint16_t* orow = out + (((int64_t)b * Hq + (int64_t)kvh * nrep + hd) * Lq + qd) * D;
 #pragma unroll
-      for (int c = 0; c < DC; c++) orow[16 * c + ln] = (uint16_t)Conv<T>::to_bits(oacc[c][i] * inv);
+        for (int c = 0; c < DC; c++) orow[16 * c + ln] = (uint16_t)Conv<T>::to_bits(oacc[c][i] * inv);
+      } else {  // (U, M in log2 units, L) of row (hd, qd) for the merge kernel
+        const int64_t prow = (((int64_t)b * Hkv + kvh) * nsplit + sp) * ((int64_t)nrep * Lq) + (int64_t)hd * Lq + qd;
+#pragma unroll
+        for (int c = 0; c < DC; c++) part_o[prow * D + 16 * c + ln] = oacc[c][i];
+        if (ln == 0) part_ml[prow] = make_float2(m_run[i] * LOG2E, lv);
+      }
     }
   }
 }
@@ -1680,14 +1771,46 @@ int launch_prefill_wide(int D, int gs, const void* q, int B, int Hq, int Hkv, in
                         Geometry geo, int causal, int window, float scale, void* out, hipStream_t s) {
   const int nrep = Hq / Hkv;
   const int64_t rows = (int64_t)Lq * nrep;
+  // Fewer row blocks than CUs (one 4-wave workgroup fills a CU): split each
+  // row block's keys over nsplit workgroups, at least 8 tiles of 32 keys
+  // each, and merge their partials with the decode merge kernel.
+  const int64_t span = geo.valid_len ? geo.cap : geo.n_kv;
+  const int64_t wgs = (rows + 63) / 64 * Hkv * B;
+  const int64_t cus = mlxq::device_cu_count();
+  int nsplit = 1;
+  if (wgs < cus && rows * D < ((int64_t)1 << 31)) {
+    const int64_t by_cus = (cus + wgs - 1) / wgs, by_keys = span / (8 * 32);
+    nsplit = (int)std::max<int64_t>(1, std::min<int64_t>(std::min(by_cus, by_keys), MERGE_WAVES));
+  }
+  float* part_o = nullptr;
+  float2* part_ml = nullptr;
+  if (nsplit > 1) {
+    const size_t slots = (size_t)B * Hkv * nsplit;
+    const size_t obytes = (slots * rows * D * sizeof(float) + 255) & ~(size_t)255;
+    void* pws = nullptr;
+    uint32_t* unused_counters = nullptr;
+    int rc = mlxq::workspace(obytes + slots * rows * sizeof(float2), 0, &unused_counters, &pws, s);
+    if (rc) return rc;
+    part_o = (float*)pws;
+    part_ml = (float2*)((uint8_t*)pws + obytes);
+  }
 #define PREW(DV, GV)                                                                                           \
   if (D == DV && gs == GV) {                                                                                   \
     using SH = PrefillWideShape<DV, GV, BITS>;                                                                 \
-    dim3 grid((unsigned)((rows + SH::ROWS - 1) / SH::ROWS), (unsigned)Hkv, (unsigned)B);                       \
+    static_assert(SH::ROWS == 64 && SH::TK == 32, "split sizing above");                                       \
+    dim3 grid((unsigned)((rows + SH::ROWS - 1) / SH::ROWS * nsplit), (unsigned)Hkv, (unsigned)B);              \
     hipLaunchKernelGGL((sdpa_prefill_wide_kernel<T, BITS, DV, GV>), grid, dim3(SH::NT), 0, s,                  \
                        (const uint16_t*)q, kp, (const uint16_t*)ks, (const uint16_t*)kb, vp, (const uint16_t*)vs, \
-                       (const uint16_t*)vb, Hq, Hkv, Lq, geo, causal, window, scale, (uint16_t*)out);          \
+                       (const uint16_t*)vb, Hq, Hkv, Lq, geo, causal, window, scale, (uint16_t*)out, nsplit,   \
+                       part_o, part_ml);                                                                       \
     MLXQ_LAUNCHED("sdpa_prefill_wide_kernel");                                                                 \
+    if (nsplit > 1) {                                                                                          \
+      const int64_t cols = rows * D / 4;                                                                       \
+      dim3 mgrid((unsigned)((cols + 63) / 64), (unsigned)Hkv, (unsigned)B);                                    \
+      hipLaunchKernelGGL((sdpa_decode_merge_kernel<T>), mgrid, dim3(64 * nsplit), 0, s, (const float4*)part_o, \
+                         part_ml, (int)(Hq * (int64_t)Lq), Hkv, D, geo, 0, nsplit, (uint16_t*)out);           \
+      MLXQ_LAUNCHED("sdpa_decode_merge_kernel");                                                               \
+    }                                                                                                          \
     return MLXQ_OK;                                                                                            \
   }
   PREW(256, 32) PREW(256, 64) PREW(256, 128) PREW(512, 64) PREW(512, 128)
@@ -1871,7 +1994,7 @@ int launch_decode(const void* q, int B, int Hq, int Hkv, const uint32_t* kp, con
   if (nchunks > 1) {
     const int cols = nrep * D / 4;
     dim3 mgrid((unsigned)((cols + 63) / 64), (unsigned)Hkv, (unsigned)B);
-    hipLaunchKernelGGL((sdpa_decode_merge_kernel<T>), mgrid, dim3(256), 0, s, (const float4*)part_o, part_ml, Hq,
+    hipLaunchKernelGGL((sdpa_decode_merge_kernel<T>), mgrid, dim3(MERGE_WAVES * 64), 0, s, (const float4*)part_o, part_ml, Hq,
                        Hkv, D, geo, chunk, (int)nchunks, (uint16_t*)out);
     MLXQ_LAUNCHED("sdpa_decode_merge_kernel");
   }
@@ -1931,7 +2054,7 @@ int launch_decode_wide(const void* q, int B, int Hq, int Hkv, const uint32_t* kp
   if (nchunks > 1) {
     const int cols = nrep * D / 4;
     dim3 mgrid((unsigned)((cols + 63) / 64), (unsigned)Hkv, (unsigned)B);
-    hipLaunchKernelGGL((sdpa_decode_merge_kernel<T>), mgrid, dim3(256), 0, s, (const float4*)part_o, part_ml, Hq,
+    hipLaunchKernelGGL((sdpa_decode_merge_kernel<T>), mgrid, dim3(MERGE_WAVES * 64), 0, s, (const float4*)part_o, part_ml, Hq,
                        Hkv, D, geo, chunk, (int)nchunks, (uint16_t*)out);
     MLXQ_LAUNCHED("sdpa_decode_merge_kernel");
   }

@@ -138,7 +138,9 @@ def test_decode_wide_ring(O, mlxq_dev):
     (1, 16, 2, 33, 300, 512, 128, 8, F16, 1.0, 0),      # group 128, 8-bit
     (2, 8, 2, 40, 257, 256, 32, 4, BF16, 0.0625, 0),    # D 256, 8 groups, batch 2
     (1, 4, 4, 129, 129, 256, 64, 8, BF16, 0.0625, 50),  # prompt (queries = keys) under a window
-    (1, 8, 1, 17, 2000, 512, 64, 4, BF16, 1.0, 0),      # short chunk over a long cache
+    (1, 8, 1, 17, 2000, 512, 64, 4, BF16, 1.0, 0),      # short chunk over a long cache (keys split 7 ways)
+    (1, 16, 2, 24, 4096, 512, 64, 4, BF16, 1.0, 1000),  # 16 key splits under a window: empty and fully masked splits
+    (2, 8, 1, 9, 3000, 256, 32, 8, F16, 0.0625, 0),     # batch 2, 11 key splits
 ])
 def test_prefill_wide(O, mlxq_dev, B, Hq, Hkv, L, N, D, gs, bits, dtype, scale, window):
     """Chunked prefill at head_dim 256 / 512 (the wide MFMA kernel: 16 rows
