@@ -559,25 +559,23 @@ __global__ void __launch_bounds__(512) sdpa_decode_mfma_kernel(
 // Split-K merge: out[b, kvh*nrep + h, d] = sum_c U_c e^{M_c - M} / sum_c L_c e^{M_c - M}
 // over the chunks c of row b (the reference's deterministic flash-decoding
 // merge, src/model/fused-decode-kernel.ts:205-222).  Workgroup (cb, kvh, b)
-// owns 64 float4 columns of (h, d); its waves (blockDim.x / 64, at most
-// MERGE_WAVES) fold the chunks c = wave, wave + waves, ... with an online
-// merge and combine in LDS in fixed order (16 waves: a 128-chunk row keeps
-// 8 loads in flight per wave instead of walking 32).  chunk > 0: the chunks
+// owns 64 float4 columns of (h, d); its NWM waves (~8 chunks each, see
+// launch_merge) fold the chunks c = wave, wave + NWM, ... with an online
+// merge and combine in LDS in fixed order.  chunk > 0: the chunks
 // are the decode chunks of row b (rows whose keys fit one chunk were
 // finished by the partial kernel); chunk == 0: every row has nslots chunks
 // (the split prefill, whose rows h are (head, query) pairs in output order).
 // A chunk with no unmasked key (M = -inf) adds nothing; a row with none
 // at all stores 0, as the single-pass kernels do.
-constexpr int MERGE_WAVES = 16;
-template <typename T>
-__global__ void __launch_bounds__(MERGE_WAVES * 64) sdpa_decode_merge_kernel(const float4* __restrict__ part_o,
+template <typename T, int NWM>
+__global__ void __launch_bounds__(NWM * 64) sdpa_decode_merge_kernel(const float4* __restrict__ part_o,
                                                                 const float2* __restrict__ part_ml, int Hq, int Hkv,
                                                                 int D, Geometry geo, int chunk, int nslots,
                                                                 uint16_t* __restrict__ out) {
-  __shared__ float4 ul[MERGE_WAVES][64];
-  __shared__ float2 mll[MERGE_WAVES][64];
+  __shared__ float4 ul[NWM][64];
+  __shared__ float2 mll[NWM][64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int nw = (int)(blockDim.x >> 6);
+  constexpr int nw = NWM;
   const int b = blockIdx.z, kvh = blockIdx.y;
   const int nrep = Hq / Hkv;
   const int cols = nrep * D / 4;
@@ -596,9 +594,12 @@ __global__ void __launch_bounds__(MERGE_WAVES * 64) sdpa_decode_merge_kernel(con
   for (int cc = wave; cc < nch; cc += nw) {
     const float2 ml = pml[cc * nrep + h];
     const float4 u = po[(int64_t)cc * cols + colc];
-    if (ml.x == -INFINITY) continue;  // fully masked chunk (its L and U are 0)
-    const float Mn = fmaxf(M, ml.x);
-    const float a = __builtin_amdgcn_exp2f(M - Mn), f = __builtin_amdgcn_exp2f(ml.x - Mn);  // M = -inf -> a = 0
+    // a fully masked chunk (M = -inf, L = U = 0) leaves the fold as it is;
+    // selects, not a branch, so the unrolled loads stay ahead of the math
+    const bool live = ml.x != -INFINITY;
+    const float Mn = live ? fmaxf(M, ml.x) : M;
+    const float a = live ? __builtin_amdgcn_exp2f(M - Mn) : 1.0f;  // M = -inf -> a = 0
+    const float f = live ? __builtin_amdgcn_exp2f(ml.x - Mn) : 0.0f;
     L = L * a + ml.y * f;
     U.x = U.x * a + u.x * f;
     U.y = U.y * a + u.y * f;
@@ -611,9 +612,11 @@ __global__ void __launch_bounds__(MERGE_WAVES * 64) sdpa_decode_merge_kernel(con
   lds_barrier();
   if (wave != 0 || !active) return;
   float Mt = -INFINITY;
+#pragma unroll
   for (int w = 0; w < nw; w++) Mt = fmaxf(Mt, mll[w][lane].x);
   float Lt = 0.f;
   float4 Ut = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
   for (int w = 0; w < nw; w++) {
     const float mw = mll[w][lane].x;
     const float f = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - Mt);  // wave with no chunk adds 0
@@ -630,6 +633,28 @@ __global__ void __launch_bounds__(MERGE_WAVES * 64) sdpa_decode_merge_kernel(con
   Conv<T>::store(out, o + 1, any ? Ut.y / Lt : 0.f);
   Conv<T>::store(out, o + 2, any ? Ut.z / Lt : 0.f);
   Conv<T>::store(out, o + 3, any ? Ut.w / Lt : 0.f);
+}
+
+// Merge of up to nslots chunks per row: ~8 chunks a wave (the fold's
+// unroll), 2 to 16 waves.
+template <typename T>
+int launch_merge(dim3 grid, int64_t nslots, hipStream_t s, const float* part_o, const float2* part_ml, int Hq,
+                  int Hkv, int D, Geometry geo, int chunk, uint16_t* out) {
+  const int64_t want = (nslots + 7) / 8;
+#define MERGE_AT(W)                                                                                              \
+  hipLaunchKernelGGL((sdpa_decode_merge_kernel<T, W>), grid, dim3(64 * W), 0, s, (const float4*)part_o, part_ml, \
+                     Hq, Hkv, D, geo, chunk, (int)nslots, out)
+  if (want <= 2)
+    MERGE_AT(2);
+  else if (want <= 4)
+    MERGE_AT(4);
+  else if (want <= 8)
+    MERGE_AT(8);
+  else
+    MERGE_AT(16);
+#undef MERGE_AT
+  MLXQ_LAUNCHED("sdpa_decode_merge_kernel");
+  return MLXQ_OK;
 }
 
 // ===================================================== MFMA decode, wide rows
@@ -1780,7 +1805,7 @@ int launch_prefill_wide(int D, int gs, const void* q, int B, int Hq, int Hkv, in
   int nsplit = 1;
   if (wgs < cus && rows * D < ((int64_t)1 << 31)) {
     const int64_t by_cus = (cus + wgs - 1) / wgs, by_keys = span / (8 * 32);
-    nsplit = (int)std::max<int64_t>(1, std::min<int64_t>(std::min(by_cus, by_keys), MERGE_WAVES));
+    nsplit = (int)std::max<int64_t>(1, std::min<int64_t>(std::min(by_cus, by_keys), 16));
   }
   float* part_o = nullptr;
   float2* part_ml = nullptr;
@@ -1807,9 +1832,9 @@ int launch_prefill_wide(int D, int gs, const void* q, int B, int Hq, int Hkv, in
     if (nsplit > 1) {                                                                                          \
       const int64_t cols = rows * D / 4;                                                                       \
       dim3 mgrid((unsigned)((cols + 63) / 64), (unsigned)Hkv, (unsigned)B);                                    \
-      hipLaunchKernelGGL((sdpa_decode_merge_kernel<T>), mgrid, dim3(64 * nsplit), 0, s, (const float4*)part_o, \
-                         part_ml, (int)(Hq * (int64_t)Lq), Hkv, D, geo, 0, nsplit, (uint16_t*)out);           \
-      MLXQ_LAUNCHED("sdpa_decode_merge_kernel");                                                               \
+      const int mrc = launch_merge<T>(mgrid, nsplit, s, part_o, part_ml, (int)(Hq * (int64_t)Lq), Hkv, D, geo, \
+                                      0, (uint16_t*)out);                                                      \
+      if (mrc) return mrc;                                                                                     \
     }                                                                                                          \
     return MLXQ_OK;                                                                                            \
   }
@@ -1994,9 +2019,7 @@ int launch_decode(const void* q, int B, int Hq, int Hkv, const uint32_t* kp, con
   if (nchunks > 1) {
     const int cols = nrep * D / 4;
     dim3 mgrid((unsigned)((cols + 63) / 64), (unsigned)Hkv, (unsigned)B);
-    hipLaunchKernelGGL((sdpa_decode_merge_kernel<T>), mgrid, dim3(MERGE_WAVES * 64), 0, s, (const float4*)part_o, part_ml, Hq,
-                       Hkv, D, geo, chunk, (int)nchunks, (uint16_t*)out);
-    MLXQ_LAUNCHED("sdpa_decode_merge_kernel");
+    return launch_merge<T>(mgrid, nchunks, s, part_o, part_ml, Hq, Hkv, D, geo, chunk, (uint16_t*)out);
   }
   return MLXQ_OK;
 }
@@ -2054,9 +2077,7 @@ int launch_decode_wide(const void* q, int B, int Hq, int Hkv, const uint32_t* kp
   if (nchunks > 1) {
     const int cols = nrep * D / 4;
     dim3 mgrid((unsigned)((cols + 63) / 64), (unsigned)Hkv, (unsigned)B);
-    hipLaunchKernelGGL((sdpa_decode_merge_kernel<T>), mgrid, dim3(MERGE_WAVES * 64), 0, s, (const float4*)part_o, part_ml, Hq,
-                       Hkv, D, geo, chunk, (int)nchunks, (uint16_t*)out);
-    MLXQ_LAUNCHED("sdpa_decode_merge_kernel");
+    return launch_merge<T>(mgrid, nchunks, s, part_o, part_ml, Hq, Hkv, D, geo, chunk, (uint16_t*)out);
   }
   return MLXQ_OK;
 }
