@@ -76,6 +76,8 @@ __global__ void __launch_bounds__(512) qmv_kernel(const uint16_t* __restrict__ x
   constexpr float OFF = CO::OFFSET;
   constexpr int WIN = qmv_window<MB>();
   static_assert(QG <= 2 && NGW % 4 == 0, "tile / group geometry");
+  // K need not be a whole number of tiles: the last tile's lanes past K read
+  // the next row's codes (or 0 past the matrix) against x slots staged as 0
   extern __shared__ __align__(16) uint8_t smem[];
   const int tid = threadIdx.x, lane = tid & 63, nw = blockDim.x >> 6;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar offsets need it
@@ -86,7 +88,7 @@ __global__ void __launch_bounds__(512) qmv_kernel(const uint16_t* __restrict__ x
   bm.resolve(bidx, xb, xok, wb, wok);
   const int n0 = blockIdx.x * 16 * R;
   const int rows = wok ? min(16 * R, N - n0) : 0;
-  const int G = K / GS, KT = K / TILE_K;
+  const int G = K / GS, KT = (K + TILE_K - 1) / TILE_K;
   const uint32_t row_bytes = (uint32_t)K * BITS / 8;
   x += xb * M * K;
   y += (int64_t)bidx * M * N;
@@ -120,17 +122,36 @@ __global__ void __launch_bounds__(512) qmv_kernel(const uint16_t* __restrict__ x
     xst[c] = buf_load128(rx, off, 0u);
   }
   uint32_t sst[SPL][2], bst[SPL][2];
+  if (G % 4 == 0) {  // a row's 4-group chunks are 8-byte aligned
 #pragma unroll
-  for (int c = 0; c < SPL; c++) {
-    const int ci = lane + 64 * c;  // chunk ci: row ci % 16R, groups g_first + 4 (ci / 16R) ..
-    const int r = ci % (16 * R), g4 = g_first + 4 * (ci / (16 * R));
-    const uint32_t off = (ci < SCH && g4 < G) ? (uint32_t)(r * G + g4) * 2u : 0x80000000u;
-    const auto sv = __builtin_amdgcn_raw_buffer_load_b64(rs, (int)off, 0, 0);
-    const auto bv = __builtin_amdgcn_raw_buffer_load_b64(rb, (int)off, 0, 0);
-    sst[c][0] = sv[0];
-    sst[c][1] = sv[1];
-    bst[c][0] = bv[0];
-    bst[c][1] = bv[1];
+    for (int c = 0; c < SPL; c++) {
+      const int ci = lane + 64 * c;  // chunk ci: row ci % 16R, groups g_first + 4 (ci / 16R) ..
+      const int r = ci % (16 * R), g4 = g_first + 4 * (ci / (16 * R));
+      const uint32_t off = (ci < SCH && g4 < G) ? (uint32_t)(r * G + g4) * 2u : 0x80000000u;
+      const auto sv = __builtin_amdgcn_raw_buffer_load_b64(rs, (int)off, 0, 0);
+      const auto bv = __builtin_amdgcn_raw_buffer_load_b64(rb, (int)off, 0, 0);
+      sst[c][0] = sv[0];
+      sst[c][1] = sv[1];
+      bst[c][0] = bv[0];
+      bst[c][1] = bv[1];
+    }
+  } else {  // the same chunks one group at a time (groups past G read 0)
+#pragma unroll
+    for (int c = 0; c < SPL; c++) {
+      const int ci = lane + 64 * c;
+      const int r = ci % (16 * R), g4 = g_first + 4 * (ci / (16 * R));
+      uint32_t sv[4], bv[4];
+#pragma unroll
+      for (int gi = 0; gi < 4; gi++) {
+        const uint32_t off = (ci < SCH && g4 + gi < G) ? (uint32_t)(r * G + g4 + gi) * 2u : 0x80000000u;
+        sv[gi] = buf_load16(rs, off, 0u);
+        bv[gi] = buf_load16(rb, off, 0u);
+      }
+      sst[c][0] = (sv[0] & 0xffffu) | (sv[1] << 16);
+      sst[c][1] = (sv[2] & 0xffffu) | (sv[3] << 16);
+      bst[c][0] = (bv[0] & 0xffffu) | (bv[1] << 16);
+      bst[c][1] = (bv[2] & 0xffffu) | (bv[3] << 16);
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
 
@@ -251,11 +272,13 @@ __global__ void __launch_bounds__(512) qmv_kernel(const uint16_t* __restrict__ x
 #pragma unroll
     for (int rb = 0; rb < MB; rb++) red[(wave * R * MB + ri * MB + rb) * 64 + lane] = yacc[ri][rb];
   lds_barrier();
-  if (wave < R * MB) {
-    const int ri = wave / MB, rb = wave % MB;
-    f32x4_t acc = red[wave * 64 + lane];
+  // output block ob = (ri, rb) is summed and stored by wave ob % nw (a wave
+  // takes several blocks when K gave fewer waves than R * MB blocks)
+  for (int ob = wave; ob < R * MB; ob += nw) {
+    const int ri = ob / MB, rb = ob % MB;
+    f32x4_t acc = red[ob * 64 + lane];
     for (int wv = 1; wv < nw; wv++) {
-      const f32x4_t o = red[(wv * R * MB + wave) * 64 + lane];
+      const f32x4_t o = red[(wv * R * MB + ob) * 64 + lane];
       acc[0] += o[0];
       acc[1] += o[1];
       acc[2] += o[2];
@@ -697,14 +720,15 @@ int qmv_tpw_override() {
 bool plan_qmv(int bits, int gs, int64_t M, int64_t K, int64_t N, int64_t batch, QmvPlan* p) {
   const int tile_k = 512 / bits;
   const int qg = tile_k > gs ? tile_k / gs : 1;
-  const int64_t G = K / gs;
-  // scales stage in 8-byte chunks of 4 groups
-  if (K % tile_k || K % gs || qg > 2 || G % 4) return false;
+  // whole groups (so 16-byte weight rows and 8-value x chunks); a last
+  // partial tile and a group count that is not a multiple of 4 are handled
+  // in the kernel
+  if (K % gs || qg > 2) return false;
   const int64_t rows = M * qg;
   p->MB = rows <= 16 ? 1 : (rows <= 32 ? 2 : 0);
   if (!p->MB) return false;
   p->MR = (p->MB == 1 && rows <= 2) ? 2 : 4;
-  const int64_t kt = K / tile_k;
+  const int64_t kt = (K + tile_k - 1) / tile_k;
   p->TPW = 0;
   const int ov = qmv_tpw_override();
   for (int tpw : {4, 8, 16}) {

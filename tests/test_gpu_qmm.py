@@ -70,6 +70,16 @@ def test_qmv_qmm_down_proj(O, mlxq_dev, w_down, M):
     (BF16, 4, 128, 2, 77, 2048),
     (BF16, 8, 128, 33, 64, 256),
     (F16, 4, 128, 64, 50, 1280),
+    # qmv with K not a whole number of 128-code tiles and / or a group count
+    # that is not a multiple of 4 (scales staged one group at a time)
+    (BF16, 4, 64, 1, 2816, 704),   # MoE down projection of the 26B-A4B model: 5.5 tiles, 11 groups
+    (F16, 4, 64, 3, 100, 320),     # 2.5 tiles, 5 groups
+    (BF16, 8, 64, 2, 90, 704),     # 8-bit: whole tiles, 11 groups
+    (BF16, 4, 128, 1, 64, 640),    # group 128: 5 groups
+    (F16, 4, 64, 16, 70, 448),     # two row blocks, 3.5 tiles, 7 groups
+    # one wave for several output blocks (K of 2 tiles): each block stored
+    (BF16, 4, 64, 16, 40, 256),    # 2 row blocks
+    (F16, 4, 64, 12, 8192, 256),   # 2 row blocks x 2 row tiles
 ])
 def test_qmm_mfma_variants(O, mlxq_dev, dtype, bits, gs, M, N, K):
     w = rng_t(O, (N, K), 3, dtype, 0.05)
