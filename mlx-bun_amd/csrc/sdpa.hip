@@ -50,7 +50,9 @@ __device__ __forceinline__ int64_t row_valid(const Geometry& g, int b) {
 // first physical slot of row b's logical window
 __device__ __forceinline__ int64_t row_base_slot(const Geometry& g, int b, int64_t valid) {
   if (!g.ring_off) return 0;
-  int64_t s = ((int64_t)g.ring_off[b] - valid) % g.cap;
+  // (ring_off - valid) mod cap with one 32-bit remainder (cap < 2^31)
+  int64_t s = (int64_t)(g.ring_off[b] % (int32_t)g.cap) - valid;  // in (-2 cap, cap)
+  s = s < 0 ? s + g.cap : s;
   return s < 0 ? s + g.cap : s;
 }
 
@@ -74,19 +76,19 @@ __device__ __forceinline__ uint16_t group_bits(const uint32_t (&o)[(G + 1) / 2],
 }
 
 // One cache row's G group scales (or biases): 2G contiguous bytes.
-template <int G>
+template <int G, int AUX = 0>
 __device__ __forceinline__ void load_row_groups_buf(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
                                                     uint32_t (&o)[(G + 1) / 2]) {
   if constexpr (G == 1) {
-    o[0] = __builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, (int)soff, 0);
+    o[0] = __builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, (int)soff, AUX);
   } else if constexpr (G == 2) {
-    o[0] = __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0);
+    o[0] = __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, AUX);
   } else if constexpr (G == 4) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, (int)soff, 0);
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, (int)soff, AUX);
     o[0] = v[0];
     o[1] = v[1];
   } else {
-    const u32x4_t v = buf_load128(r, voff, soff);
+    const u32x4_t v = buf_load128<AUX>(r, voff, soff);
     o[0] = v.x;
     o[1] = v.y;
     o[2] = v.z;
@@ -117,14 +119,18 @@ struct ChunkRange {
   int nk, nch;
 };
 
+// `chunk` is a power of two (the launchers only halve it from one), so the
+// divisions are shifts: 64-bit division would expand to a few hundred
+// instructions ahead of every workgroup's first load.
 __device__ __forceinline__ ChunkRange chunk_range(const Geometry& geo, int b, int chunk, int c) {
   ChunkRange r;
+  const int sh = __builtin_ctz((unsigned)chunk);
+  const int64_t cm = chunk - 1;
   const int64_t valid = row_valid(geo, b);
-  const int64_t base = row_base_slot(geo, b, valid);
+  const int64_t base = row_base_slot(geo, b, valid);  // in [0, cap)
   const int64_t jw = geo.cap - base;                  // first logical key stored at slot 0
-  const int64_t off = jw < valid ? jw % chunk : 0;    // length of a leading short chunk (0: none)
-  r.nch = valid == 0 ? 0
-                     : (off == 0 ? (int)((valid + chunk - 1) / chunk) : 1 + (int)((valid - off + chunk - 1) / chunk));
+  const int64_t off = jw < valid ? (jw & cm) : 0;     // length of a leading short chunk (0: none)
+  r.nch = valid == 0 ? 0 : (off == 0 ? (int)((valid + cm) >> sh) : 1 + (int)((valid - off + cm) >> sh));
   r.j0 = off == 0 ? (int64_t)c * chunk : (c == 0 ? 0 : off + (int64_t)(c - 1) * chunk);
   const int64_t end = (off != 0 && c == 0) ? off : min(r.j0 + chunk, valid);
   r.nk = (int)(end - r.j0);
@@ -268,7 +274,7 @@ __global__ void __launch_bounds__(512) sdpa_decode_mfma_kernel(
     const int t = 2 * p + shalf;
     const uint32_t voff = t < TPW ? (uint32_t)((wave_u + NW * t) * 32 + skey) * (2 * G) : 0x80000000u;
 #pragma unroll
-    for (int a = 0; a < 4; a++) load_row_groups_buf<G>(rsb[a], voff, 0u, sbreg[p][a]);
+    for (int a = 0; a < 4; a++) load_row_groups_buf<G, LOAD_STREAM>(rsb[a], voff, 0u, sbreg[p][a]);
   }
   __builtin_amdgcn_sched_barrier(0);  // issue order: scales/biases, then codes
 
@@ -283,7 +289,7 @@ __global__ void __launch_bounds__(512) sdpa_decode_mfma_kernel(
       const uint32_t soff = (kt + 16u * sub) * (uint32_t)(KW * 4);
 #pragma unroll
       for (int w4 = 0; w4 < LKW; w4 += 4) {
-        const u32x4_t v = buf_load128(rk, voff + 4u * w4, soff);
+        const u32x4_t v = buf_load128<LOAD_STREAM>(rk, voff + 4u * w4, soff);
         kb[sub][w4] = v.x;
         kb[sub][w4 + 1] = v.y;
         kb[sub][w4 + 2] = v.z;
@@ -298,13 +304,13 @@ __global__ void __launch_bounds__(512) sdpa_decode_mfma_kernel(
       const uint32_t voff = (koff * KW + VM * ln) * 4u;
       const uint32_t soff = kt * (uint32_t)(KW * 4);
       if constexpr (VM == 1) {
-        vb[e][0] = buf_load32(rv, voff, soff);
+        vb[e][0] = buf_load32<LOAD_STREAM>(rv, voff, soff);
       } else if constexpr (VM == 2) {
-        const auto v = __builtin_amdgcn_raw_buffer_load_b64(rv, (int)voff, (int)soff, 0);
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(rv, (int)voff, (int)soff, LOAD_STREAM);
         vb[e][0] = v[0];
         vb[e][1] = v[1];
       } else {
-        const u32x4_t v = buf_load128(rv, voff, soff);
+        const u32x4_t v = buf_load128<LOAD_STREAM>(rv, voff, soff);
         vb[e][0] = v.x;
         vb[e][1] = v.y;
         vb[e][2] = v.z;
@@ -590,22 +596,32 @@ __global__ void __launch_bounds__(NWM * 64) sdpa_decode_merge_kernel(const float
   const float2* pml = part_ml + bk * nslots * nrep;
   float M = -INFINITY, L = 0.f;
   float4 U = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll 8
-  for (int cc = wave; cc < nch; cc += nw) {
-    const float2 ml = pml[cc * nrep + h];
-    const float4 u = po[(int64_t)cc * cols + colc];
-    // a fully masked chunk (M = -inf, L = U = 0) leaves the fold as it is;
-    // selects, not a branch, so the unrolled loads stay ahead of the math
-    const bool live = ml.x != -INFINITY;
-    const float Mn = live ? fmaxf(M, ml.x) : M;
-    const float a = live ? __builtin_amdgcn_exp2f(M - Mn) : 1.0f;  // M = -inf -> a = 0
-    const float f = live ? __builtin_amdgcn_exp2f(ml.x - Mn) : 0.0f;
-    L = L * a + ml.y * f;
-    U.x = U.x * a + u.x * f;
-    U.y = U.y * a + u.y * f;
-    U.z = U.z * a + u.z * f;
-    U.w = U.w * a + u.w * f;
-    M = Mn;
+  // batches of 8 chunks per wave: all 16 loads of a batch are issued before
+  // any of its math (one memory round trip per batch, not one per chunk)
+  for (int c0 = wave; c0 < nch; c0 += 8 * nw) {
+    float2 ml[8];
+    float4 u[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const int cc = min(c0 + i * nw, nch - 1);  // past nch: a valid slot, not folded
+      ml[i] = pml[cc * nrep + h];
+      u[i] = po[(int64_t)cc * cols + colc];
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      // a fully masked chunk (M = -inf, L = U = 0) leaves the fold as it
+      // is; selects, not a branch, so the math waits on one load at a time
+      const bool live = c0 + i * nw < nch && ml[i].x != -INFINITY;
+      const float Mn = live ? fmaxf(M, ml[i].x) : M;
+      const float a = live ? __builtin_amdgcn_exp2f(M - Mn) : 1.0f;  // M = -inf -> a = 0
+      const float f = live ? __builtin_amdgcn_exp2f(ml[i].x - Mn) : 0.0f;
+      L = L * a + ml[i].y * f;
+      U.x = U.x * a + u[i].x * f;
+      U.y = U.y * a + u[i].y * f;
+      U.z = U.z * a + u[i].z * f;
+      U.w = U.w * a + u[i].w * f;
+      M = Mn;
+    }
   }
   ul[wave][lane] = U;
   mll[wave][lane] = make_float2(M, L);
@@ -792,14 +808,14 @@ __global__ void __launch_bounds__(512) sdpa_decode_wide_kernel(
     const uint32_t key = (uint32_t)(TK * t + 16 * wave + ln);
 #pragma unroll
     for (int j = 0; j < KI; j++) {
-      const u32x4_t v = buf_load128(rk, (key * KW + 16u * j + 4u * lq) * 4u, 0u);
+      const u32x4_t v = buf_load128<LOAD_STREAM>(rk, (key * KW + 16u * j + 4u * lq) * 4u, 0u);
       k.w[j][0] = v.x;
       k.w[j][1] = v.y;
       k.w[j][2] = v.z;
       k.w[j][3] = v.w;
     }
-    load_row_groups_buf<G>(rks, key * (uint32_t)(2 * G), 0u, k.s);
-    load_row_groups_buf<G>(rkb, key * (uint32_t)(2 * G), 0u, k.bb);
+    load_row_groups_buf<G, LOAD_STREAM>(rks, key * (uint32_t)(2 * G), 0u, k.s);
+    load_row_groups_buf<G, LOAD_STREAM>(rkb, key * (uint32_t)(2 * G), 0u, k.bb);
   };
   auto load_v = [&](int t, VSlot& v) {
 #pragma unroll
@@ -812,14 +828,14 @@ __global__ void __launch_bounds__(512) sdpa_decode_wide_kernel(
       for (int kk = 0; kk < 4; kk++) {
         const uint32_t key = (uint32_t)(TK * t + 4 * kq + kk);
         const uint32_t off = act ? (key * KW + 4u * db) * 4u : 0x80000000u;  // inactive: reads 0
-        const u32x4_t x = buf_load128(rv, off, 0u);
+        const u32x4_t x = buf_load128<LOAD_STREAM>(rv, off, 0u);
         v.w[p][kk][0] = x.x;
         v.w[p][kk][1] = x.y;
         v.w[p][kk][2] = x.z;
         v.w[p][kk][3] = x.w;
         const uint32_t so = act ? ((key * (uint32_t)G + (uint32_t)vg) * 2u) & ~3u : 0x80000000u;
-        v.s[p][kk] = __builtin_amdgcn_raw_buffer_load_b32(rvs, (int)so, 0, 0);
-        v.bb[p][kk] = __builtin_amdgcn_raw_buffer_load_b32(rvb, (int)so, 0, 0);
+        v.s[p][kk] = __builtin_amdgcn_raw_buffer_load_b32(rvs, (int)so, 0, LOAD_STREAM);
+        v.bb[p][kk] = __builtin_amdgcn_raw_buffer_load_b32(rvb, (int)so, 0, LOAD_STREAM);
       }
     }
   };
@@ -1997,6 +2013,7 @@ int launch_decode(const void* q, int B, int Hq, int Hkv, const uint32_t* kp, con
     while (chunk > 128 && ((span + chunk - 1) / chunk) * B * Hkv < cus) chunk /= 2;
   }
   // a ring row's window may start mid-chunk at the wrap point: one extra chunk
+  MLXQ_CHECK((chunk & (chunk - 1)) == 0, "decode chunk must be a power of two");
   const int64_t nchunks = (span > 0 ? (span + chunk - 1) / chunk : 1) + (geo.ring_off ? 1 : 0);
   MLXQ_CHECK(nchunks < 65536, "kv length too large for one launch");
   void* pws = nullptr;
@@ -2055,6 +2072,7 @@ int launch_decode_wide(const void* q, int B, int Hq, int Hkv, const uint32_t* kp
     const int64_t cus = mlxq::device_cu_count();
     while (chunk > SH::TK && ((span + chunk - 1) / chunk) * B * Hkv < cus) chunk /= 2;
   }
+  MLXQ_CHECK((chunk & (chunk - 1)) == 0, "decode chunk must be a power of two");
   const int64_t nchunks = (span > 0 ? (span + chunk - 1) / chunk : 1) + (geo.ring_off ? 1 : 0);
   MLXQ_CHECK(nchunks < 65536, "kv length too large for one launch");
   void* pws = nullptr;
