@@ -708,10 +708,18 @@ struct QmvPlan {
   size_t lds;
 };
 
-// MLXQ_QMV_TPW (4, 8 or 16) overrides the tiles each wave streams.
+// MLXQ_QMV_TPW (4, 8 or 16) overrides the tiles each wave streams,
+// MLXQ_QMV_R (1 or 2) the 16-row weight tiles per workgroup.
 int qmv_tpw_override() {
   static const int v = [] {
     const char* e = getenv("MLXQ_QMV_TPW");
+    return e ? atoi(e) : 0;
+  }();
+  return v;
+}
+int qmv_r_override() {
+  static const int v = [] {
+    const char* e = getenv("MLXQ_QMV_R");
     return e ? atoi(e) : 0;
   }();
   return v;
@@ -738,9 +746,28 @@ bool plan_qmv(int bits, int gs, int64_t M, int64_t K, int64_t N, int64_t batch, 
     }
   }
   if (!p->TPW) return false;
-  p->NW = (int)((kt + p->TPW - 1) / p->TPW);
   // two row tiles per workgroup when that still gives every CU a workgroup
-  p->R = ((N + 31) / 32) * batch >= (int64_t)mlxq::device_cu_count() ? 2 : 1;
+  const int64_t cus = mlxq::device_cu_count();
+  p->R = ((N + 31) / 32) * batch >= cus ? 2 : 1;
+  if (rows <= 2 && ov == 0) {
+    // One activation row: each wave's stream as long as possible while the
+    // launch keeps >= 7 waves per CU and wastes <= 1/8 of its tiles on
+    // clamped duplicates, then two row tiles per workgroup if the count
+    // still holds (MI355X, 4-bit: x[1, 4096] @ W[14336, 4096]^T 10.1 ->
+    // 9.2 us with 16 tiles a wave; the 262144 x 2816 head 93 -> 79 us with 8
+    // tiles a wave and two row tiles)
+    auto waves = [&](int tpw, int r) { return ((N + 16 * r - 1) / (16 * r)) * batch * ((kt + tpw - 1) / tpw); };
+    for (int tpw : {16, 8, 4}) {
+      const int64_t nw = (kt + tpw - 1) / tpw;
+      if (nw > 8 || (int64_t)tpw * tile_k / gs % 4 != 0 || 8 * (nw * tpw - kt) > kt) continue;
+      if (tpw != 4 && waves(tpw, 1) < 7 * cus) continue;
+      p->TPW = tpw;
+      p->R = waves(tpw, 2) >= 7 * cus ? 2 : 1;
+      break;
+    }
+  }
+  if (qmv_r_override() == 1 || qmv_r_override() == 2) p->R = qmv_r_override();
+  p->NW = (int)((kt + p->TPW - 1) / p->TPW);
   const int64_t xpw = (int64_t)p->TPW * tile_k, ngw = xpw / gs;
   const size_t wave_lds = (size_t)M * xpw * 2 + (size_t)ngw * 16 * p->R * 8;
   const size_t rbytes = (size_t)p->NW * p->R * p->MB * 64 * 16;
