@@ -170,12 +170,22 @@ struct DecodeShape {
   static constexpr int KW = D * BITS / 32;   // packed words per cache row
   static constexpr int G = D / GS;
   // tiles (32 keys) per wave: up to 128/KW, with the chunk's fp32
-  // scales/biases (16 G bytes per key) held to 32 KB of LDS
+  // scales/biases (16 G bytes per key) held to 32 KB of LDS, 64 KB from 4
+  // groups a row on (D 256 at group 64: 4 tiles a wave instead of 2, half the
+  // chunks; the 32-row batched ring decode 102 -> 86 us on MI355X)
   static constexpr int TPW_REG = 128 / KW;
-  static constexpr int TPW_LDS = 2048 / (G * NW * 32);
+  static constexpr int TPW_LDS = (G >= 4 ? 4096 : 2048) / (G * NW * 32);
   static constexpr int TPW = TPW_REG < TPW_LDS ? TPW_REG : TPW_LDS;
   static constexpr int MAXC = NW * 32 * TPW;  // keys per workgroup
   static constexpr int WIN = MLXQ_DECODE_WINDOW;  // tiles in flight per wave
+  // Lazy softmax rescale: the running max moves only when a tile exceeds it
+  // by more than LAZY (log2 units).  At 4 groups a row with 4 tiles a wave
+  // the lazy rule (p up to 2^8) widened the error tail at scale 1 (32-row
+  // ring decode, D 256: 44 outputs past 0.01 against 1 with eager
+  // rescaling), so those instances rescale on every new max; at D 128 both
+  // rules measure the same error (scale 1 and 1/sqrt(128)) and lazy is
+  // 0.4 us faster on the 32k decode.
+  static constexpr float LAZY = G >= 4 ? 0.0f : 8.0f;
 };
 
 // One workgroup = NW waves = one chunk of up to MAXC keys of one (batch row,
@@ -415,10 +425,10 @@ __global__ void __launch_bounds__(512) sdpa_decode_mfma_kernel(
     float tmax = fmaxf(fmaxf(fmaxf(s2[0], s2[1]), fmaxf(s2[2], s2[3])), fmaxf(fmaxf(s2[4], s2[5]), fmaxf(s2[6], s2[7])));
     tmax = xrow_max(tmax);
     // Lazy rescale: keep the reference max unless this tile exceeds it by
-    // more than 2^8 (p stays <= 256, fp32 and T both hold that exactly as a
-    // scale); the accumulators are only rewritten when it moves.
+    // more than SH::LAZY (p stays <= 2^LAZY, fp32 and T both hold that
+    // exactly as a scale); the accumulators are only rewritten when it moves.
     const float m_old = m_run;
-    const float m_new = tmax > m_old + 8.0f ? tmax : m_old;  // first tile: m_old = -inf
+    const float m_new = tmax > m_old + SH::LAZY ? tmax : m_old;  // first tile: m_old = -inf
     const float alpha = __builtin_amdgcn_exp2f(m_old - m_new);  // 1 unless moved; -inf -> 0
     m_run = m_new;
     float p[8];
