@@ -754,8 +754,8 @@ bool plan_qmv(int bits, int gs, int64_t M, int64_t K, int64_t N, int64_t batch, 
     // launch keeps >= 7 waves per CU and wastes <= 1/8 of its tiles on
     // clamped duplicates, then two row tiles per workgroup if the count
     // still holds (MI355X, 4-bit: x[1, 4096] @ W[14336, 4096]^T 10.1 ->
-    // 9.2 us with 16 tiles a wave; the 262144 x 2816 head 93 -> 79 us with 8
-    // tiles a wave and two row tiles)
+    // 9.2 us with 16 tiles a wave; the 262144 x 2816 head 101 -> 88 us with
+    // 8 tiles a wave and two row tiles)
     auto waves = [&](int tpw, int r) { return ((N + 16 * r - 1) / (16 * r)) * batch * ((kt + tpw - 1) / tpw); };
     for (int tpw : {16, 8, 4}) {
       const int64_t nw = (kt + tpw - 1) / tpw;
