@@ -50,8 +50,11 @@ __device__ __forceinline__ int64_t row_valid(const Geometry& g, int b) {
 // first physical slot of row b's logical window
 __device__ __forceinline__ int64_t row_base_slot(const Geometry& g, int b, int64_t valid) {
   if (!g.ring_off) return 0;
-  // (ring_off - valid) mod cap with one 32-bit remainder (cap < 2^31)
-  int64_t s = (int64_t)(g.ring_off[b] % (int32_t)g.cap) - valid;  // in (-2 cap, cap)
+  // (ring_off - valid) mod cap with at most one 32-bit remainder: an int32
+  // offset is its own remainder once cap >= 2^31
+  const int32_t r = g.ring_off[b];
+  const int64_t rm = g.cap < ((int64_t)1 << 31) ? (int64_t)(r % (int32_t)g.cap) : (int64_t)r;  // |rm| < cap
+  int64_t s = rm - valid;  // in (-2 cap, cap)
   s = s < 0 ? s + g.cap : s;
   return s < 0 ? s + g.cap : s;
 }
