@@ -15,6 +15,9 @@ Also measured in the same run and reported beside it:
                         U[512, 32768] and ring offsets U[0, 4096), 4-bit
   qmv_qmm               x [M, 4096] @ W[14336, 4096]^T and x [M, 14336] @
                         W[4096, 14336]^T, 4-bit group 64, M in {1, 4, 16, 64}
+  moe_gather_prefill_sorted  gather_qmm over a 512-token chunk's 4096 rows in
+                        expert order (SwitchGLU's sorted call), gate_up shape,
+                        beside the per-row gather of the same rows
   moe_gather_decode     gather_qmm of one decode token against top-8 of 128
                         stacked 4-bit experts: gate_up [1408, 2816] and down
                         [2816, 704] (the 26B-A4B expert shapes)
@@ -268,6 +271,53 @@ def moe_gather_workload(N, K, E=128, topk=8, B=1, gs=64, bits=4, seed=60, nsets=
     return launch, algo, (parts, idx, xmap, xs, y)
 
 
+def moe_sorted_workload(N, K, E=128, tokens=512, topk=8, gs=64, bits=4, seed=90):
+    """SwitchGLU over a prefill chunk: tokens x topk (row, expert) pairs,
+    rows gathered in expert order (x [rows, 1, K], indices sorted), against
+    E stacked 4-bit experts [E, N, K] (16 quantized experts copied into the E
+    slots).  Returns launchers for the sorted (grouped GEMM) and the per-row
+    gather over the same rows, and the algorithmic bytes (each present
+    expert once, x in, y out)."""
+    from mlxq import _lib, ops
+    from mlxq.array import DeviceArray
+
+    src = ops.quantize(rand_t((16, N, K), seed, BF16, 0.02), gs, bits)
+    parts = []
+    for a in (src.packed, src.scales, src.biases):
+        full = DeviceArray.empty((E,) + a.shape[1:], a.dtype)
+        per = a.nbytes // 16
+        for e in range(E):
+            _lib.call("mlxq_memcpy_dtod", full.ptr + e * per, a.ptr + (e % 16) * per, per, None)
+        parts.append(full)
+    src.dispose()
+    wp, ws, wb = parts
+    r = np.random.default_rng(seed + 1)
+    sel = np.stack([r.choice(E, topk, replace=False) for _ in range(tokens)]).ravel()
+    idx_h = np.sort(sel).astype(np.uint32)
+    rows = idx_h.size
+    idx = DeviceArray.fromNumpy(idx_h, 3)
+    x = rand_t((rows, 1, K), seed + 2)
+    y = DeviceArray.empty((rows, 1, N), BF16)
+    L = _lib.lib()
+
+    def sorted_launch(i):
+        rc = L.mlxq_gather_qmm_sorted(x.ptr, BF16, rows, K, idx.ptr, wp.ptr, ws.ptr, wb.ptr, E, N, gs, bits, y.ptr,
+                                      None)
+        if rc:
+            raise RuntimeError(L.mlxq_last_error().decode())
+
+    def per_row_launch(i):
+        rc = L.mlxq_gather_qmm(x.ptr, BF16, rows, rows, 1, K, None, idx.ptr, wp.ptr, ws.ptr, wb.ptr, E, N, gs, bits,
+                               1, y.ptr, None)
+        if rc:
+            raise RuntimeError(L.mlxq_last_error().decode())
+
+    expert_bytes = N * K * bits // 8 + 2 * 2 * N * (K // gs)
+    algo = len(np.unique(idx_h)) * expert_bytes + rows * K * 2 + rows * N * 2
+    flops = 2 * rows * N * K
+    return sorted_launch, per_row_launch, algo, flops, (parts, idx, x, y)
+
+
 # ------------------------------------------------------------- tied head
 
 def tied_head_workload(vocab=262144, H=2816, gs=64, bits=4, seed=80):
@@ -421,6 +471,16 @@ def main():
                          "pct_hbm_peak": round(100 * bm / (msm * 1e-3) / 1e9 / HBM_PEAK_GBS, 1)}
             del km
         extra["moe_gather_decode"] = moe
+        log("bench: MoE gather_qmm, sorted prefill rows")
+        ls_, lr_, bs_, fs_, ks_ = moe_sorted_workload(1408, 2816)
+        mss = timer.graph_step_ms(ls_, 20, 3)
+        msr = timer.graph_step_ms(lr_, 5, 1)
+        extra["moe_gather_prefill_sorted"] = {
+            "workload": "gate_up [1408, 2816] 4-bit, 512 tokens x top-8 of 128 experts = 4096 rows in expert order",
+            "us_per_call": round(mss * 1e3, 2), "per_row_us_per_call": round(msr * 1e3, 2),
+            "algorithmic_bytes": bs_, "GB/s": round(bs_ / (mss * 1e-3) / 1e9, 1),
+            "TFLOP/s": round(fs_ / (mss * 1e-3) / 1e12, 1)}
+        del ks_
         log("bench: tied head")
         lh, bh, kh = tied_head_workload()
         msh = timer.graph_step_ms(lh, 50, 5)

@@ -170,12 +170,28 @@ int mlxq_quantized_matmul(const void* x, int dtype, int64_t batch, int64_t M, in
  * src/model/gemma4.ts:434-438); NULL means x_map[i] = i (x_batch == batch).
  * rhs_indices: [batch] uint32 on the device.  An index outside [0, x_batch)
  * or [0, n_experts) yields a zero output row (MLX leaves it undefined).
- * sorted_indices (a scheduling hint in MLX) has no counterpart: results do
- * not depend on it.  y: [batch, M, N] T, fp32 accumulation. */
+ * sorted_indices (a scheduling hint in MLX) is mlxq_gather_qmm_sorted
+ * below; results do not depend on it.  y: [batch, M, N] T, fp32
+ * accumulation. */
 int mlxq_gather_qmm(const void* x, int dtype, int64_t x_batch, int64_t batch, int64_t M, int64_t K,
                     const int32_t* x_map, const uint32_t* rhs_indices, const uint32_t* w, const void* scales,
                     const void* biases, int64_t n_experts, int64_t N, int group_size, int bits, int transpose,
                     void* y, void* stream);
+
+/* gatherQmm(x, w, scales, biases, rhsIndices, spec, sortedIndices = true)
+ * -- the call of src/mlx/ops.ts:186-204 with sorted_indices set, as
+ * SwitchGLU makes it once a batch has 64 or more (row, expert) pairs: rows
+ * gathered in expert order first (_gather_sort, src/model/gemma4.ts:441-464),
+ * so x is [rows, 1, K] with row i using expert rhs_indices[i] (transpose=1,
+ * no x map).  Rows with equal consecutive indices run as one GEMM block, so
+ * an expert's weights stream once per block rather than once per row.
+ * Results equal mlxq_gather_qmm's over the same rows (up to fp32 summation
+ * order) whatever the index order; unsorted indices are only slower.  Index
+ * range and zero rows as mlxq_gather_qmm.  Uses the library's workspace
+ * (1 + 3 rows int32) on `stream`.  y: [rows, 1, N] T. */
+int mlxq_gather_qmm_sorted(const void* x, int dtype, int64_t rows, int64_t K, const uint32_t* rhs_indices,
+                           const uint32_t* w, const void* scales, const void* biases, int64_t n_experts,
+                           int64_t N, int group_size, int bits, void* y, void* stream);
 
 /* ------------------------------------------------------------------ sdpa */
 

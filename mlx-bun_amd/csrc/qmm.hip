@@ -25,6 +25,7 @@
 // everything else (transpose = false, 2-bit, fp32 activations) the VALU
 // kernel below.  All three resolve a batch element through a BatchMap, which
 // also serves mx.gather_qmm (an x row map and an expert index per element).
+#include <algorithm>
 #include <cstdlib>
 
 #include "mfma_common.h"
@@ -36,10 +37,16 @@ namespace {
 // An index outside [0, x_batch) / [0, n_w) marks the element's x rows or
 // weights as absent: the kernels then read zeros (zero-sized descriptors),
 // so the output rows are zeros and no access leaves the arrays.
+//
+// Work-list mode (seg != null, the tiled GEMM only): seg[0] items, item j =
+// (seg[1 + 3j], seg[2 + 3j], seg[3 + 3j]) = (first row, rows, weight index)
+// over x / y rows stored one after another (x_batch rows in all) -- the
+// sorted rows of mx.gather_qmm, grouped by expert by qmm_segments_kernel.
 struct BatchMap {
   const int32_t* x_map;
   const uint32_t* w_idx;
   int64_t x_batch, n_w, w_rep;
+  const int32_t* seg = nullptr;
   __device__ __forceinline__ void resolve(int64_t b, int64_t& xb, bool& xok, int64_t& wb, bool& wok) const {
     xb = x_map ? (int64_t)x_map[b] : b;
     wb = w_idx ? (int64_t)w_idx[b] : b / w_rep;
@@ -354,15 +361,35 @@ __global__ void __launch_bounds__(256) qmm_tile_kernel(const uint16_t* __restric
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / SH::WGN, wn = wave % SH::WGN;
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-  const int bidx = blockIdx.z / KS, split = blockIdx.z % KS;
-  int64_t xb, wb;
+  // one pass (z = blockIdx.z) unless a work list is given: then items z,
+  // z + gridDim.z, ... (KS = 1 there; every row block of the list is
+  // computed whatever the grid, also for a list longer than it)
+  const int nz = bm.seg ? bm.seg[0] : (int)gridDim.z;
+  for (int z = blockIdx.z; z < nz; z += gridDim.z) {
+  const int bidx = z / KS, split = z % KS;
+  int64_t xb = 0, wb, xrow0, yrow0;
   bool xok, wok;
-  bm.resolve(bidx, xb, xok, wb, wok);
+  int Mi = M;
+  if (bm.seg) {
+    const int32_t* it = bm.seg + 1 + 3 * (int64_t)z;
+    xrow0 = it[0];
+    Mi = it[1];
+    wb = it[2];
+    xok = xrow0 >= 0 && Mi >= 1 && Mi <= BM && xrow0 + Mi <= bm.x_batch;
+    wok = wb >= 0 && wb < bm.n_w;
+    if (!xok) xrow0 = 0, Mi = 0;  // nothing read, nothing stored
+    if (!wok) wb = 0;
+    yrow0 = xrow0;
+  } else {
+    bm.resolve(bidx, xb, xok, wb, wok);
+    xrow0 = xb * M;
+    yrow0 = (int64_t)bidx * M;
+  }
   const int G = K / GS, KT = K / BK;
   const int kb = split * KTS, ke = min(KT, kb + KTS);
   const uint32_t row_bytes = (uint32_t)K * BITS / 8;
-  const int mrows = xok ? min(BM, M - m0) : 0, nrows = wok ? min(BN, N - n0) : 0;
-  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + (xb * M + m0) * K, (uint32_t)(mrows * K * 2));
+  const int mrows = xok ? min(BM, Mi - m0) : 0, nrows = wok ? min(BN, N - n0) : 0;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + (xrow0 + m0) * K, (uint32_t)(max(mrows, 0) * K * 2));
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(w + ((int64_t)wb * N + n0) * (row_bytes / 4), (uint32_t)nrows * row_bytes);
   // scales / biases: whole arrays (4-byte aligned), read as the dword that
   // holds the wanted 16-bit value (a 16-bit load feeding the prefetch ring
@@ -553,14 +580,78 @@ __global__ void __launch_bounds__(256) qmm_tile_kernel(const uint16_t* __restric
 #pragma unroll
       for (int v = 0; v < 16; v++) {
         const int m = m0 + wm * WM + 32 * i + 8 * (v / 4) + 4 * lh + v % 4;
-        if (m < M && n < N) {
+        if (m < Mi && n < N) {
           if (KS == 1)
-            y[((int64_t)bidx * M + m) * N + n] = (uint16_t)Conv<T>::to_bits(acc[i][j][v]);
+            y[(yrow0 + m) * N + n] = (uint16_t)Conv<T>::to_bits(acc[i][j][v]);
           else
             part[(((int64_t)split * gridDim.z / KS + bidx) * M + m) * N + n] = acc[i][j][v];
         }
       }
     }
+  }  // work items
+}
+
+// Work list of mx.gather_qmm over sorted rows: rows with equal consecutive
+// indices form one expert's run, cut into blocks of at most BM rows; item j
+// = (first row, rows, expert) at seg[1 + 3j], the count at seg[0] (at most
+// R items).  One workgroup walks the rows 1024 at a time: a max-scan of run
+// starts gives each row's run start, a sum-scan numbers the block starts.
+// Unsorted indices only give shorter runs (every row still lands in one item).
+__global__ void __launch_bounds__(1024) qmm_segments_kernel(const uint32_t* __restrict__ idx, int R, int BM,
+                                                            int32_t* __restrict__ seg) {
+  __shared__ int sc[1024];
+  __shared__ int carry_start, carry_count;
+  const int tid = threadIdx.x;
+  if (tid == 0) carry_start = 0, carry_count = 0;
+  __syncthreads();
+  for (int base = 0; base < R; base += 1024) {
+    const int r = base + tid;
+    const bool valid = r < R;
+    const uint32_t cur = valid ? idx[r] : 0u;
+    const bool st = valid && (r == 0 || idx[r - 1] != cur);
+    int v = st ? r : -1;  // inclusive max-scan: latest run start at or before r in this chunk
+    sc[tid] = v;
+    __syncthreads();
+    for (int off = 1; off < 1024; off <<= 1) {
+      const int o = tid >= off ? sc[tid - off] : -1;
+      __syncthreads();
+      v = max(v, o);
+      sc[tid] = v;
+      __syncthreads();
+    }
+    const int rs = v >= 0 ? v : carry_start;
+    const bool f = valid && (r - rs) % BM == 0;  // a block starts here
+    int c = f ? 1 : 0;  // inclusive sum-scan of block starts
+    __syncthreads();
+    sc[tid] = c;
+    __syncthreads();
+    for (int off = 1; off < 1024; off <<= 1) {
+      const int o = tid >= off ? sc[tid - off] : 0;
+      __syncthreads();
+      c += o;
+      sc[tid] = c;
+      __syncthreads();
+    }
+    if (f) {
+      const int pos = carry_count + c - 1;
+      int n = 1;
+      while (n < BM && r + n < R && idx[r + n] == cur) n++;
+      seg[1 + 3 * pos] = r;
+      seg[2 + 3 * pos] = n;
+      seg[3 + 3 * pos] = (int32_t)cur;
+    }
+    const int total = sc[1023];
+    const int last = min(R - base, 1024) - 1;  // this chunk's last valid row
+    int last_rs = 0;
+    if (tid == last) last_rs = rs;
+    __syncthreads();  // every thread has read carry_start / carry_count and sc
+    if (tid == last) {
+      carry_start = last_rs;
+      carry_count += total;
+    }
+    __syncthreads();
+  }
+  if (tid == 0) seg[0] = carry_count;
 }
 
 // y = T(sum over splits of the fp32 partials), fixed split order.
@@ -911,6 +1002,79 @@ extern "C" int mlxq_quantized_matmul(const void* x, int dtype, int64_t batch, in
   if (K == 0) return mlxq_fill_zero(y, (uint64_t)(batch * M * N * mlxq::dtype_bytes(dtype)), stream);
   const BatchMap bm{nullptr, nullptr, batch, w_batch, batch / w_batch};
   return qmm_dispatch(x, dtype, batch, M, K, w, scales, biases, bm, N, group_size, bits, transpose, y, s);
+}
+
+// Sorted gather: rows of equal consecutive expert index run as one GEMM
+// block (<= BM rows) of the tiled kernel, so each expert's weights stream
+// once per block instead of once per row.
+template <typename T, int BITS, int GS, int BM>
+int launch_qmm_sorted_inst(const void* x, int64_t R, int64_t K, const uint32_t* w, const void* scales,
+                           const void* biases, const uint32_t* idx, int64_t n_experts, int64_t N, void* y,
+                           hipStream_t s) {
+  void* p = nullptr;
+  uint32_t* unused_counters = nullptr;
+  int rc = mlxq::workspace((1 + 3 * (size_t)R) * sizeof(int32_t), 0, &unused_counters, &p, s);
+  if (rc) return rc;
+  int32_t* seg = (int32_t*)p;
+  hipLaunchKernelGGL(qmm_segments_kernel, dim3(1), dim3(1024), 0, s, idx, (int)R, BM, seg);
+  MLXQ_LAUNCHED("qmm_segments_kernel");
+  // sorted rows give at most R / BM + (experts present) items; a longer list
+  // (unsorted rows) is walked by the same workgroups
+  const int64_t slots = std::min<int64_t>(std::min<int64_t>(R, (R + BM - 1) / BM + n_experts), 65535);
+  BatchMap bm{nullptr, idx, R, n_experts, 1, seg};
+  dim3 grid((unsigned)((N + 127) / 128), 1, (unsigned)slots);
+  hipLaunchKernelGGL((qmm_tile_kernel<T, BITS, GS, BM, 128>), grid, dim3(256), 0, s, (const uint16_t*)x, 1, (int)K,
+                     w, (const uint16_t*)scales, (const uint16_t*)biases, (int)N, bm, 1, (int)(K / 64),
+                     (uint32_t)(((n_experts * N * (K / GS)) * 2 + 3) & ~(int64_t)3), (uint16_t*)y, nullptr);
+  MLXQ_LAUNCHED("qmm_tile_kernel");
+  return MLXQ_OK;
+}
+
+template <typename T, int BITS, int GS>
+int launch_qmm_sorted(const void* x, int64_t R, int64_t K, const uint32_t* w, const void* scales, const void* biases,
+                      const uint32_t* idx, int64_t n_experts, int64_t N, void* y, hipStream_t s) {
+  if (R >= 48 * n_experts)
+    return launch_qmm_sorted_inst<T, BITS, GS, 64>(x, R, K, w, scales, biases, idx, n_experts, N, y, s);
+  return launch_qmm_sorted_inst<T, BITS, GS, 32>(x, R, K, w, scales, biases, idx, n_experts, N, y, s);
+}
+
+extern "C" int mlxq_gather_qmm_sorted(const void* x, int dtype, int64_t rows, int64_t K, const uint32_t* rhs_indices,
+                                      const uint32_t* w, const void* scales, const void* biases, int64_t n_experts,
+                                      int64_t N, int group_size, int bits, void* y, void* stream) {
+  const int64_t batch = rows, M = 1;
+  const int transpose = 1;
+  QMM_COMMON_CHECKS();
+  MLXQ_CHECK(n_experts >= 1, "n_experts must be >= 1");
+  MLXQ_CHECK(rows <= 0x7fffffff, "too many rows");
+  if (rows == 0 || N == 0) return MLXQ_OK;
+  MLXQ_CHECK(x && w && scales && biases && y && rhs_indices, "null buffer");
+  hipStream_t s = mlxq::resolve_stream(stream);
+  if (K == 0) return mlxq_fill_zero(y, (uint64_t)(rows * N * mlxq::dtype_bytes(dtype)), stream);
+  const bool seg_ok = rows >= 2 * n_experts && mlxq::is_half_dtype(dtype) && (bits == 4 || bits == 8) &&
+                      K % 64 == 0 && (uintptr_t)x % 16 == 0 && (uintptr_t)w % 16 == 0 &&
+                      (uintptr_t)scales % 4 == 0 && (uintptr_t)biases % 4 == 0 && 64 * K * 2 < ((int64_t)1 << 31) &&
+                      N * K < ((int64_t)1 << 31) && n_experts * N * (K / group_size) * 2 < ((int64_t)1 << 31);
+  if (seg_ok) {
+#define QMM_SORTED_T(TT)                                                                                         \
+  switch (bits * 1000 + group_size) {                                                                           \
+    case 4032: return launch_qmm_sorted<TT, 4, 32>(x, rows, K, w, scales, biases, rhs_indices, n_experts, N, y, s); \
+    case 4064: return launch_qmm_sorted<TT, 4, 64>(x, rows, K, w, scales, biases, rhs_indices, n_experts, N, y, s); \
+    case 4128: return launch_qmm_sorted<TT, 4, 128>(x, rows, K, w, scales, biases, rhs_indices, n_experts, N, y, s); \
+    case 8032: return launch_qmm_sorted<TT, 8, 32>(x, rows, K, w, scales, biases, rhs_indices, n_experts, N, y, s); \
+    case 8064: return launch_qmm_sorted<TT, 8, 64>(x, rows, K, w, scales, biases, rhs_indices, n_experts, N, y, s); \
+    default: return launch_qmm_sorted<TT, 8, 128>(x, rows, K, w, scales, biases, rhs_indices, n_experts, N, y, s); \
+  }
+    if (dtype == MLXQ_BFLOAT16) {
+      QMM_SORTED_T(BF16)
+    } else {
+      QMM_SORTED_T(F16)
+    }
+#undef QMM_SORTED_T
+  }
+  // few rows a expert (or a layout the tiled kernel does not take): one row
+  // per batch element, as the unsorted gather
+  const BatchMap bm{nullptr, rhs_indices, rows, n_experts, 1};
+  return qmm_dispatch(x, dtype, rows, 1, K, w, scales, biases, bm, N, group_size, bits, 1, y, s);
 }
 
 extern "C" int mlxq_gather_qmm(const void* x, int dtype, int64_t x_batch, int64_t batch, int64_t M, int64_t K,

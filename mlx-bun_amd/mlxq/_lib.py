@@ -26,7 +26,7 @@ SYMBOLS = (
     "mlxq_event_create", "mlxq_event_destroy", "mlxq_event_record", "mlxq_event_elapsed_ms",
     "mlxq_graph_begin", "mlxq_graph_end", "mlxq_graph_launch", "mlxq_graph_destroy",
     "mlxq_quantize", "mlxq_kv_append", "mlxq_dequantize", "mlxq_embedding_gather", "mlxq_quantized_matmul",
-    "mlxq_gather_qmm",
+    "mlxq_gather_qmm", "mlxq_gather_qmm_sorted",
     "mlxq_quantized_sdpa",
 )
 
@@ -69,6 +69,7 @@ def _declare(L: ctypes.CDLL) -> None:
         "mlxq_embedding_gather": [P, I64, P, P, P, I, I64, I64, I, I, P, P],
         "mlxq_quantized_matmul": [P, I, I64, I64, I64, P, P, P, I64, I64, I, I, I, P, P],
         "mlxq_gather_qmm": [P, I, I64, I64, I64, I64, P, P, P, P, P, I64, I64, I, I, I, P, P],
+        "mlxq_gather_qmm_sorted": [P, I, I64, I64, P, P, P, P, I64, I64, I, I, P, P],
         "mlxq_quantized_sdpa": [P, I, I, I, I, I, I, P, P, P, P, P, P, I64, I64, P, P, I, I, F, I, I, P, P],
     }
     for name, args in sig.items():

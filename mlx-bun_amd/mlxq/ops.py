@@ -142,9 +142,12 @@ def gatherQmm(x: DeviceArray, w: DeviceArray, scales: DeviceArray, biases: Optio
     rhsIndices (uint32 or int32) selects the expert per output batch element,
     its shape broadcasting with x's leading dims.  Returns
     broadcast(x[..., :-2], rhsIndices) + [M, N] in x's dtype.  sortedIndices
-    is MLX's scheduling hint; results do not depend on it."""
+    is MLX's scheduling hint, results do not depend on it: for SwitchGLU's
+    sorted call (rows gathered in expert order, x [rows, 1, K], indices
+    [rows], src/model/gemma4.ts:441-473) it runs each expert's rows as GEMM
+    blocks (mlxq_gather_qmm_sorted) instead of one matrix-vector product a
+    row."""
     _check_mode(spec.mode)
-    del sortedIndices
     if biases is None:
         raise ValueError("affine gather_qmm requires biases")
     for a, n in ((x, "x"), (w, "w"), (scales, "scales"), (biases, "biases"), (rhsIndices, "rhsIndices")):
@@ -183,9 +186,13 @@ def gatherQmm(x: DeviceArray, w: DeviceArray, scales: DeviceArray, biases: Optio
         idx = DeviceArray.fromNumpy(np.ascontiguousarray(host), rhsIndices.dtype)
         keep.append(idx)
     y = DeviceArray.empty(out_lead + (M, N), x.dtype)
-    _lib.call("mlxq_gather_qmm", x.ptr, x.dtype, x_batch, batch, M, K, x_map.ptr if x_map is not None else None,
-              idx.ptr, w.ptr, scales.ptr, biases.ptr, E, N, spec.groupSize, spec.bits, int(bool(transpose)), y.ptr,
-              None)
+    if sortedIndices and transpose and M == 1 and x_map is None:
+        _lib.call("mlxq_gather_qmm_sorted", x.ptr, x.dtype, batch, K, idx.ptr, w.ptr, scales.ptr, biases.ptr, E, N,
+                  spec.groupSize, spec.bits, y.ptr, None)
+    else:
+        _lib.call("mlxq_gather_qmm", x.ptr, x.dtype, x_batch, batch, M, K,
+                  x_map.ptr if x_map is not None else None, idx.ptr, w.ptr, scales.ptr, biases.ptr, E, N,
+                  spec.groupSize, spec.bits, int(bool(transpose)), y.ptr, None)
     # the temporaries are freed (hipFree, which waits for the device) only
     # after the launch that reads them
     del keep

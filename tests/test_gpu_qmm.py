@@ -151,7 +151,7 @@ def _gather_ref(O, x, wq, idx_flat, x_map, gs, bits, dtype):
     return np.stack(out)
 
 
-def _gather(O, x, wq, idx, gs, bits, dtype, idx_dtype=3):
+def _gather(O, x, wq, idx, gs, bits, dtype, idx_dtype=3, sorted_indices=False):
     from mlxq import ops
     from mlxq.array import DeviceArray
 
@@ -159,7 +159,7 @@ def _gather(O, x, wq, idx, gs, bits, dtype, idx_dtype=3):
     y = ops.gatherQmm(DeviceArray.fromFloat32(x, x.shape, dtype), DeviceArray.fromNumpy(p, 3),
                       DeviceArray.fromNumpy(s, dtype), DeviceArray.fromNumpy(b, dtype),
                       DeviceArray.fromNumpy(np.asarray(idx, np.uint32 if idx_dtype == 3 else np.int32), idx_dtype),
-                      ops.QuantSpec(bits, gs), False)
+                      ops.QuantSpec(bits, gs), sorted_indices)
     return y.toFloat32()
 
 
@@ -233,3 +233,64 @@ def test_gather_qmm_many_rows_per_expert(O, mlxq_dev, experts_up):
     got = _gather(O, x, experts_up, idx, 64, 4, BF16)
     ref = _gather_ref(O, x, experts_up, idx, [0, 1], 64, 4, BF16)
     assert_close(got, ref, what="tile gather", dtype=BF16)
+
+
+# ------------------------------------------------- gather_qmm, sorted rows
+
+@pytest.fixture(scope="module")
+def experts_small(O):
+    """16 experts W [256, 512] ~ N(0, 0.02^2), 4-bit group 64, with their
+    float64 dequantization."""
+    w = rng_t(O, (16, 256, 512), 41, BF16, 0.02)
+    wq = O.quantize(w, 64, 4, BF16)
+    wd = np.stack([deq64(O, wq[0][e], wq[1][e], wq[2][e], 64, 4, BF16) for e in range(16)])
+    return wq, wd
+
+
+def _sorted_ref(x, wd, idx):
+    """out[i] = x[i] @ deq(W[idx[i]])^T (an index past the experts: zeros)."""
+    xf = x.reshape(len(idx), -1).astype(np.float64)
+    out = np.zeros((len(idx), wd.shape[1]))
+    for e in np.unique(idx):
+        if 0 <= e < len(wd):
+            rows = np.nonzero(idx == e)[0]
+            out[rows] = xf[rows] @ wd[e].T
+    return out.reshape(len(idx), 1, -1)
+
+
+@pytest.mark.parametrize("rows,order", [(512, "sorted"), (2048, "sorted"), (512, "unsorted"), (300, "one expert")])
+def test_gather_qmm_sorted_grouped_gemm(O, mlxq_dev, experts_small, rows, order):
+    """SwitchGLU's sorted call (src/model/gemma4.ts:441-473): x [rows, 1, K]
+    in expert order, indices [rows], sortedIndices=True -> expert runs as GEMM
+    blocks (32-row blocks at 512 rows over 16 experts, 64-row blocks at 2048,
+    runs longer than a block).  Unsorted indices with the flag set and a
+    single expert's run give the same results; equal to the per-row gather."""
+    wq, wd = experts_small
+    r = np.random.default_rng(rows)
+    if order == "one expert":
+        idx = np.full(rows, 7, np.uint32)
+    else:
+        idx = r.integers(0, 16, rows).astype(np.uint32)
+        if order == "sorted":
+            idx.sort()
+    x = rng_t(O, (rows, 1, 512), 60 + rows, BF16)
+    got = _gather(O, x, wq, idx, 64, 4, BF16, sorted_indices=True)
+    assert_close(got, _sorted_ref(x, wd, idx), what=f"sorted gather {rows} {order}", dtype=BF16)
+    per_row = _gather(O, x, wq, idx, 64, 4, BF16)
+    assert_close(got, per_row, atol=1e-2, rtol=1e-3, what="sorted vs per-row", dtype=BF16)
+
+
+def test_gather_qmm_sorted_bad_index_and_repeat(O, mlxq_dev, experts_small):
+    """Sorted rows whose last run indexes past the experts give zero rows, and
+    a second, smaller call through the same workspace is still exact."""
+    wq, wd = experts_small
+    idx = np.sort(np.random.default_rng(5).integers(0, 16, 640)).astype(np.uint32)
+    idx[-40:] = 99
+    x = rng_t(O, (640, 1, 512), 77, BF16)
+    got = _gather(O, x, wq, idx, 64, 4, BF16, sorted_indices=True)
+    assert not got[-40:].any()
+    assert_close(got, _sorted_ref(x, wd, idx), what="sorted bad index", dtype=BF16)
+    idx2 = np.sort(np.random.default_rng(6).integers(0, 16, 96)).astype(np.uint32)
+    x2 = rng_t(O, (96, 1, 512), 78, BF16)
+    got2 = _gather(O, x2, wq, idx2, 64, 4, BF16, sorted_indices=True)
+    assert_close(got2, _sorted_ref(x2, wd, idx2), what="sorted second call", dtype=BF16)
