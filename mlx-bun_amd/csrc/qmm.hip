@@ -331,7 +331,7 @@ struct TileShape {
   static_assert(TM >= 1 && TN >= 1 && WM % 32 == 0 && WN % 32 == 0, "tile shape");
 };
 
-template <typename T, int BITS, int GS, int BM, int BN>
+template <typename T, int BITS, int GS, int BM, int BN, bool SEG = false>
 __global__ void __launch_bounds__(256) qmm_tile_kernel(const uint16_t* __restrict__ x, int M, int K,
                                                        const uint32_t* __restrict__ w,
                                                        const uint16_t* __restrict__ scales,
@@ -361,16 +361,16 @@ __global__ void __launch_bounds__(256) qmm_tile_kernel(const uint16_t* __restric
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / SH::WGN, wn = wave % SH::WGN;
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-  // one pass (z = blockIdx.z) unless a work list is given: then items z,
-  // z + gridDim.z, ... (KS = 1 there; every row block of the list is
-  // computed whatever the grid, also for a list longer than it)
-  const int nz = bm.seg ? bm.seg[0] : (int)gridDim.z;
-  for (int z = blockIdx.z; z < nz; z += gridDim.z) {
+  // One item (z = blockIdx.z), or with a work list (SEG, KS = 1) items z,
+  // z + gridDim.z, ...: every row block of the list is computed whatever the
+  // grid, also for a list longer than it.
+  const int z_end = SEG ? bm.seg[0] : (int)blockIdx.z + 1;
+  for (int z = blockIdx.z; z < z_end; z += SEG ? (int)gridDim.z : 1) {
   const int bidx = z / KS, split = z % KS;
   int64_t xb = 0, wb, xrow0, yrow0;
   bool xok, wok;
   int Mi = M;
-  if (bm.seg) {
+  if constexpr (SEG) {
     const int32_t* it = bm.seg + 1 + 3 * (int64_t)z;
     xrow0 = it[0];
     Mi = it[1];
@@ -383,13 +383,13 @@ __global__ void __launch_bounds__(256) qmm_tile_kernel(const uint16_t* __restric
   } else {
     bm.resolve(bidx, xb, xok, wb, wok);
     xrow0 = xb * M;
-    yrow0 = (int64_t)bidx * M;
+    yrow0 = 0;  // stores index (bidx, m) directly
   }
   const int G = K / GS, KT = K / BK;
   const int kb = split * KTS, ke = min(KT, kb + KTS);
   const uint32_t row_bytes = (uint32_t)K * BITS / 8;
   const int mrows = xok ? min(BM, Mi - m0) : 0, nrows = wok ? min(BN, N - n0) : 0;
-  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + (xrow0 + m0) * K, (uint32_t)(max(mrows, 0) * K * 2));
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + (xrow0 + m0) * K, (uint32_t)(mrows * K * 2));
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(w + ((int64_t)wb * N + n0) * (row_bytes / 4), (uint32_t)nrows * row_bytes);
   // scales / biases: whole arrays (4-byte aligned), read as the dword that
   // holds the wanted 16-bit value (a 16-bit load feeding the prefetch ring
@@ -581,8 +581,10 @@ __global__ void __launch_bounds__(256) qmm_tile_kernel(const uint16_t* __restric
       for (int v = 0; v < 16; v++) {
         const int m = m0 + wm * WM + 32 * i + 8 * (v / 4) + 4 * lh + v % 4;
         if (m < Mi && n < N) {
-          if (KS == 1)
+          if constexpr (SEG)
             y[(yrow0 + m) * N + n] = (uint16_t)Conv<T>::to_bits(acc[i][j][v]);
+          else if (KS == 1)
+            y[((int64_t)bidx * M + m) * N + n] = (uint16_t)Conv<T>::to_bits(acc[i][j][v]);
           else
             part[(((int64_t)split * gridDim.z / KS + bidx) * M + m) * N + n] = acc[i][j][v];
         }
@@ -1023,7 +1025,7 @@ int launch_qmm_sorted_inst(const void* x, int64_t R, int64_t K, const uint32_t* 
   const int64_t slots = std::min<int64_t>(std::min<int64_t>(R, (R + BM - 1) / BM + n_experts), 65535);
   BatchMap bm{nullptr, idx, R, n_experts, 1, seg};
   dim3 grid((unsigned)((N + 127) / 128), 1, (unsigned)slots);
-  hipLaunchKernelGGL((qmm_tile_kernel<T, BITS, GS, BM, 128>), grid, dim3(256), 0, s, (const uint16_t*)x, 1, (int)K,
+  hipLaunchKernelGGL((qmm_tile_kernel<T, BITS, GS, BM, 128, true>), grid, dim3(256), 0, s, (const uint16_t*)x, 1, (int)K,
                      w, (const uint16_t*)scales, (const uint16_t*)biases, (int)N, bm, 1, (int)(K / 64),
                      (uint32_t)(((n_experts * N * (K / GS)) * 2 + 3) & ~(int64_t)3), (uint16_t*)y, nullptr);
   MLXQ_LAUNCHED("qmm_tile_kernel");
