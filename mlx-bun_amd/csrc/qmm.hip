@@ -594,61 +594,64 @@ __global__ void __launch_bounds__(256) qmm_tile_kernel(const uint16_t* __restric
 }
 
 // Work list of mx.gather_qmm over sorted rows: rows with equal consecutive
-// indices form one expert's run, cut into blocks of at most BM rows; item j
-// = (first row, rows, expert) at seg[1 + 3j], the count at seg[0] (at most
-// R items).  One workgroup walks the rows 1024 at a time: a max-scan of run
-// starts gives each row's run start, a sum-scan numbers the block starts.
-// Unsorted indices only give shorter runs (every row still lands in one item).
+// indices form one expert's run, cut into blocks of at most BM (<= 128)
+// rows; item j = (first row, rows, expert) at seg[1 + 3j], the count at
+// seg[0] (at most R items).  One workgroup walks the rows 1024 at a time,
+// each chunk's indices (and BM after it) staged in LDS: a max-scan of run
+// starts gives each row's run start, a sum-scan numbers the block starts
+// (lane shuffles within a wave, then the 16 wave totals).  Unsorted indices
+// only give shorter runs (every row still lands in one item).
 __global__ void __launch_bounds__(1024) qmm_segments_kernel(const uint32_t* __restrict__ idx, int R, int BM,
                                                             int32_t* __restrict__ seg) {
-  __shared__ int sc[1024];
+  __shared__ uint32_t sidx[1024 + 128];
+  __shared__ int wmax[16], wsum[16];
   __shared__ int carry_start, carry_count;
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   if (tid == 0) carry_start = 0, carry_count = 0;
-  __syncthreads();
   for (int base = 0; base < R; base += 1024) {
+    for (int i = tid; i < 1024 + BM; i += 1024) sidx[i] = base + i < R ? idx[base + i] : 0u;
     const int r = base + tid;
     const bool valid = r < R;
-    const uint32_t cur = valid ? idx[r] : 0u;
-    const bool st = valid && (r == 0 || idx[r - 1] != cur);
-    int v = st ? r : -1;  // inclusive max-scan: latest run start at or before r in this chunk
-    sc[tid] = v;
+    const uint32_t before = base > 0 ? idx[base - 1] : 0u;
     __syncthreads();
-    for (int off = 1; off < 1024; off <<= 1) {
-      const int o = tid >= off ? sc[tid - off] : -1;
-      __syncthreads();
-      v = max(v, o);
-      sc[tid] = v;
-      __syncthreads();
+    const uint32_t cur = sidx[tid];
+    const bool st = valid && (r == 0 || (tid > 0 ? sidx[tid - 1] : before) != cur);
+    int v = st ? r : -1;  // inclusive max-scan: latest run start at or before r
+    int c;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int o = __shfl_up(v, off);
+      if (lane >= off) v = max(v, o);
     }
+    if (lane == 63) wmax[wave] = v;
+    __syncthreads();
+    for (int w = 0; w < wave; w++) v = max(v, wmax[w]);
     const int rs = v >= 0 ? v : carry_start;
     const bool f = valid && (r - rs) % BM == 0;  // a block starts here
-    int c = f ? 1 : 0;  // inclusive sum-scan of block starts
-    __syncthreads();
-    sc[tid] = c;
-    __syncthreads();
-    for (int off = 1; off < 1024; off <<= 1) {
-      const int o = tid >= off ? sc[tid - off] : 0;
-      __syncthreads();
-      c += o;
-      sc[tid] = c;
-      __syncthreads();
+    c = f ? 1 : 0;  // inclusive sum-scan of block starts
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int o = __shfl_up(c, off);
+      if (lane >= off) c += o;
     }
+    if (lane == 63) wsum[wave] = c;
+    __syncthreads();
+    for (int w = 0; w < wave; w++) c += wsum[w];
     if (f) {
       const int pos = carry_count + c - 1;
       int n = 1;
-      while (n < BM && r + n < R && idx[r + n] == cur) n++;
+      while (n < BM && r + n < R && sidx[tid + n] == cur) n++;
       seg[1 + 3 * pos] = r;
       seg[2 + 3 * pos] = n;
       seg[3 + 3 * pos] = (int32_t)cur;
     }
-    const int total = sc[1023];
     const int last = min(R - base, 1024) - 1;  // this chunk's last valid row
-    int last_rs = 0;
-    if (tid == last) last_rs = rs;
-    __syncthreads();  // every thread has read carry_start / carry_count and sc
+    int total = 0;
+    if (tid == last)
+      for (int w = 0; w < 16; w++) total += wsum[w];
+    __syncthreads();  // every thread is done with carry_*, wmax, wsum and sidx
     if (tid == last) {
-      carry_start = last_rs;
+      carry_start = rs;
       carry_count += total;
     }
     __syncthreads();
@@ -1013,6 +1016,7 @@ template <typename T, int BITS, int GS, int BM>
 int launch_qmm_sorted_inst(const void* x, int64_t R, int64_t K, const uint32_t* w, const void* scales,
                            const void* biases, const uint32_t* idx, int64_t n_experts, int64_t N, void* y,
                            hipStream_t s) {
+  static_assert(BM <= 128, "qmm_segments_kernel stages BM indices past each chunk");
   void* p = nullptr;
   uint32_t* unused_counters = nullptr;
   int rc = mlxq::workspace((1 + 3 * (size_t)R) * sizeof(int32_t), 0, &unused_counters, &p, s);
