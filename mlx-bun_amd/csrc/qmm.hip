@@ -366,230 +366,231 @@ __global__ void __launch_bounds__(256) qmm_tile_kernel(const uint16_t* __restric
   // grid, also for a list longer than it.
   const int z_end = SEG ? bm.seg[0] : (int)blockIdx.z + 1;
   for (int z = blockIdx.z; z < z_end; z += SEG ? (int)gridDim.z : 1) {
-  const int bidx = z / KS, split = z % KS;
-  int64_t xb = 0, wb, xrow0, yrow0;
-  bool xok, wok;
-  int Mi = M;
-  if constexpr (SEG) {
-    const int32_t* it = bm.seg + 1 + 3 * (int64_t)z;
-    xrow0 = it[0];
-    Mi = it[1];
-    wb = it[2];
-    xok = xrow0 >= 0 && Mi >= 1 && Mi <= BM && xrow0 + Mi <= bm.x_batch;
-    wok = wb >= 0 && wb < bm.n_w;
-    if (!xok) xrow0 = 0, Mi = 0;  // nothing read, nothing stored
-    if (!wok) wb = 0;
-    yrow0 = xrow0;
-  } else {
-    bm.resolve(bidx, xb, xok, wb, wok);
-    xrow0 = xb * M;
-    yrow0 = 0;  // stores index (bidx, m) directly
-  }
-  const int G = K / GS, KT = K / BK;
-  const int kb = split * KTS, ke = min(KT, kb + KTS);
-  const uint32_t row_bytes = (uint32_t)K * BITS / 8;
-  const int mrows = xok ? min(BM, Mi - m0) : 0, nrows = wok ? min(BN, N - n0) : 0;
-  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + (xrow0 + m0) * K, (uint32_t)(mrows * K * 2));
-  const __amdgpu_buffer_rsrc_t rw = make_rsrc(w + ((int64_t)wb * N + n0) * (row_bytes / 4), (uint32_t)nrows * row_bytes);
-  // scales / biases: whole arrays (4-byte aligned), read as the dword that
-  // holds the wanted 16-bit value (a 16-bit load feeding the prefetch ring
-  // would be widened, and so waited for, right at the load)
-  const __amdgpu_buffer_rsrc_t rs = make_rsrc(scales, wok ? sb_bytes : 0u);
-  const __amdgpu_buffer_rsrc_t rb = make_rsrc(biases, wok ? sb_bytes : 0u);
-  const int64_t sb_elem0 = ((int64_t)wb * N + n0) * G;  // tile's first (row, group) element
-  constexpr uint32_t OOB = 0x80000000u;  // past every descriptor: reads 0
-
-  // thread -> staging items.  x: chunk c = tid + 256 i -> row c / 8, unit
-  // c % 8 (8 values); the 8 units of a row sit in 8 adjacent lanes.
-  // codes: words [q, q + WPT) of row wr_row.  (s, b): row sb_row, part sb_e.
-  const int wr_row = tid * WPT / CWR, wr_q = tid * WPT % CWR;
-  const int sb_row = tid / NGK, sb_e = tid % NGK;
-  const bool sb_act = tid < BN * NGK;
-
-  u32x4_t xr[PF][XL];
-  uint32_t wr[PF][WPT];
-  uint32_t sr[PF], br[PF];
-  // element index of (row sb_row, group of part sb_e) in K-step kt
-  auto sb_elem = [&](int kt) -> int64_t {
-    return sb_elem0 + (int64_t)sb_row * G + ((int64_t)kt * BK + sb_e * EG) / GS;
-  };
-  // Steps past the split's end re-read its last step (never staged): a
-  // masked offset would be a uniform select, which the compiler turns into
-  // branches whose loads wait for the whole prefetch ring.
-  auto load = [&](int kt, u32x4_t (&xv)[XL], uint32_t (&wv)[WPT], uint32_t& sv, uint32_t& bv) {
-    kt = min(kt, ke - 1);
-    const uint32_t k0 = (uint32_t)kt * BK;
-#pragma unroll
-    for (int i = 0; i < XL; i++) {
-      const int c = tid + 256 * i;
-      xv[i] = buf_load128(rx, ((uint32_t)(c / 8) * (uint32_t)K + 8u * (c % 8)) * 2u, k0 * 2u);
-    }
-    const uint32_t wo = (uint32_t)wr_row * row_bytes + 4u * wr_q;
-    if constexpr (WPT == 2) {
-      const auto v = __builtin_amdgcn_raw_buffer_load_b64(rw, (int)wo, (int)(k0 * BITS / 8), 0);
-      wv[0] = v[0];
-      wv[1] = v[1];
+    const int bidx = z / KS, split = z % KS;
+    int64_t xb = 0, wb, xrow0, yrow0;
+    bool xok, wok;
+    int Mi = M;
+    if constexpr (SEG) {
+      const int32_t* it = bm.seg + 1 + 3 * (int64_t)z;
+      xrow0 = it[0];
+      Mi = it[1];
+      wb = it[2];
+      xok = xrow0 >= 0 && Mi >= 1 && Mi <= BM && xrow0 + Mi <= bm.x_batch;
+      wok = wb >= 0 && wb < bm.n_w;
+      if (!xok) xrow0 = 0, Mi = 0;  // nothing read, nothing stored
+      if (!wok) wb = 0;
+      yrow0 = xrow0;
     } else {
-#pragma unroll
-      for (int h = 0; h < WPT / 4; h++) {
-        const u32x4_t v = buf_load128(rw, wo + 16u * h, k0 * BITS / 8);
-        wv[4 * h] = v.x;
-        wv[4 * h + 1] = v.y;
-        wv[4 * h + 2] = v.z;
-        wv[4 * h + 3] = v.w;
-      }
+      bm.resolve(bidx, xb, xok, wb, wok);
+      xrow0 = xb * M;
+      yrow0 = 0;  // stores index (bidx, m) directly
     }
-    const uint32_t so = sb_act ? (uint32_t)(2 * sb_elem(kt)) & ~3u : OOB;
-    sv = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)so, 0, 0);
-    bv = __builtin_amdgcn_raw_buffer_load_b32(rb, (int)so, 0, 0);
-  };
-  auto stash = [&](const u32x4_t (&xv)[XL], const uint32_t (&wv)[WPT], uint32_t sv, uint32_t bv, int kt,
-                   int buf) {
-#pragma unroll
-    for (int i = 0; i < XL; i++) {
-      const int c = tid + 256 * i, row = c / 8, unit = c % 8;
-      *reinterpret_cast<u32x4_t*>(&xs[buf][row * PITCH + 8 * unit]) = permute8<CO::ORDER>(xv[i]);
-    }
-    const uint32_t magic = opaque(Mma<T>::MAGIC);
-#pragma unroll
-    for (int u = 0; u < UPT; u++) {
-      u32x4_t op;
-      if constexpr (BITS == 4)
-        op = CodeOps<T, 4>::operand(wv[u], magic);
-      else
-        op = CodeOps<T, BITS>::operand(wv[2 * u], wv[2 * u + 1]);
-      *reinterpret_cast<u32x4_t*>(&wc[buf][wr_row * PITCH + 8 * (wr_q / UW + u)]) = op;
-    }
-    if (sb_act) {
-      const int sh = 16 * (int)(sb_elem(kt) & 1);
-      const float sc = Conv<T>::from_bits((sv >> sh) & 0xffffu), bi = Conv<T>::from_bits((bv >> sh) & 0xffffu);
-      sbl[buf][sb_e][sb_row] = make_float2(sc, bi - OFF * sc);
-    }
-  };
+    const int G = K / GS, KT = K / BK;
+    const int kb = split * KTS, ke = min(KT, kb + KTS);
+    const uint32_t row_bytes = (uint32_t)K * BITS / 8;
+    const int mrows = xok ? min(BM, Mi - m0) : 0, nrows = wok ? min(BN, N - n0) : 0;
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + (xrow0 + m0) * K, (uint32_t)(mrows * K * 2));
+    const __amdgpu_buffer_rsrc_t rw =
+        make_rsrc(w + ((int64_t)wb * N + n0) * (row_bytes / 4), (uint32_t)nrows * row_bytes);
+    // scales / biases: whole arrays (4-byte aligned), read as the dword that
+    // holds the wanted 16-bit value (a 16-bit load feeding the prefetch ring
+    // would be widened, and so waited for, right at the load)
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(scales, wok ? sb_bytes : 0u);
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(biases, wok ? sb_bytes : 0u);
+    const int64_t sb_elem0 = ((int64_t)wb * N + n0) * G;  // tile's first (row, group) element
+    constexpr uint32_t OOB = 0x80000000u;  // past every descriptor: reads 0
 
-  f32x16_t acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; i++)
-#pragma unroll
-    for (int j = 0; j < TN; j++)
-#pragma unroll
-      for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
+    // thread -> staging items.  x: chunk c = tid + 256 i -> row c / 8, unit
+    // c % 8 (8 values); the 8 units of a row sit in 8 adjacent lanes.
+    // codes: words [q, q + WPT) of row wr_row.  (s, b): row sb_row, part sb_e.
+    const int wr_row = tid * WPT / CWR, wr_q = tid * WPT % CWR;
+    const int sb_row = tid / NGK, sb_e = tid % NGK;
+    const bool sb_act = tid < BN * NGK;
 
-  const int lr = lane & 31, lh = lane >> 5;
-  const u32x4_t ones = {Mma<T>::ONES, Mma<T>::ONES, Mma<T>::ONES, Mma<T>::ONES};
-  // A group part's fold is deferred until the next part's MFMAs are issued
-  // (where registers allow), so its VALU work overlaps the matrix core; the
-  // pending part starts as zeros (folding it adds nothing).
-  constexpr bool DEFER = TM * TN <= 2;
-  f32x16_t pd[DEFER ? TM : 1][DEFER ? TN : 1], px[DEFER ? TM : 1];
-  float2 psb[DEFER ? TN : 1];
-#pragma unroll
-  for (int i = 0; i < (DEFER ? TM : 1); i++) {
-#pragma unroll
-    for (int v = 0; v < 16; v++) px[i][v] = 0.f;
-#pragma unroll
-    for (int j = 0; j < (DEFER ? TN : 1); j++)
-#pragma unroll
-      for (int v = 0; v < 16; v++) pd[i][j][v] = 0.f;
-  }
-#pragma unroll
-  for (int j = 0; j < (DEFER ? TN : 1); j++) psb[j] = make_float2(0.f, 0.f);
-  auto fold = [&](const f32x16_t (&d)[TM][TN], const f32x16_t (&xsm)[TM], const float2 (&sb)[TN]) {
-#pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-      for (int j = 0; j < TN; j++)
-#pragma unroll
-        for (int v = 0; v < 16; v++)
-          acc[i][j][v] = __builtin_fmaf(sb[j].x, d[i][j][v], __builtin_fmaf(sb[j].y, xsm[i][v], acc[i][j][v]));
-  };
-  auto compute = [&](int buf) {
-#pragma unroll
-    for (int e = 0; e < NGK; e++) {
-      f32x16_t d[TM][TN], xsm[TM];
-#pragma unroll
-      for (int ss = 0; ss < SPG; ss++) {
-        const int kk = 16 * (e * SPG + ss) + 8 * lh;
-        u32x4_t a[TM], b[TN];
-#pragma unroll
-        for (int i = 0; i < TM; i++)
-          a[i] = *reinterpret_cast<const u32x4_t*>(&xs[buf][(wm * WM + 32 * i + lr) * PITCH + kk]);
-#pragma unroll
-        for (int j = 0; j < TN; j++)
-          b[j] = *reinterpret_cast<const u32x4_t*>(&wc[buf][(wn * WN + 32 * j + lr) * PITCH + kk]);
-        f32x16_t z;
-#pragma unroll
-        for (int v = 0; v < 16; v++) z[v] = 0.f;
-#pragma unroll
-        for (int i = 0; i < TM; i++) {
-          xsm[i] = mma32<T>(a[i], ones, ss == 0 ? z : xsm[i]);
-#pragma unroll
-          for (int j = 0; j < TN; j++) d[i][j] = mma32<T>(a[i], b[j], ss == 0 ? z : d[i][j]);
-        }
+    u32x4_t xr[PF][XL];
+    uint32_t wr[PF][WPT];
+    uint32_t sr[PF], br[PF];
+    // element index of (row sb_row, group of part sb_e) in K-step kt
+    auto sb_elem = [&](int kt) -> int64_t {
+      return sb_elem0 + (int64_t)sb_row * G + ((int64_t)kt * BK + sb_e * EG) / GS;
+    };
+    // Steps past the split's end re-read its last step (never staged): a
+    // masked offset would be a uniform select, which the compiler turns into
+    // branches whose loads wait for the whole prefetch ring.
+    auto load = [&](int kt, u32x4_t (&xv)[XL], uint32_t (&wv)[WPT], uint32_t& sv, uint32_t& bv) {
+      kt = min(kt, ke - 1);
+      const uint32_t k0 = (uint32_t)kt * BK;
+  #pragma unroll
+      for (int i = 0; i < XL; i++) {
+        const int c = tid + 256 * i;
+        xv[i] = buf_load128(rx, ((uint32_t)(c / 8) * (uint32_t)K + 8u * (c % 8)) * 2u, k0 * 2u);
       }
-      // fold: lane column n = wn WN + 32 j + lr, rows 8 (v/4) + 4 lh + v%4
-      float2 sb[TN];
-#pragma unroll
-      for (int j = 0; j < TN; j++) sb[j] = sbl[buf][e][wn * WN + 32 * j + lr];
-      if constexpr (DEFER) {
-        fold(pd, px, psb);
-#pragma unroll
-        for (int i = 0; i < TM; i++) {
-          px[i] = xsm[i];
-#pragma unroll
-          for (int j = 0; j < TN; j++) pd[i][j] = d[i][j];
-        }
-#pragma unroll
-        for (int j = 0; j < TN; j++) psb[j] = sb[j];
+      const uint32_t wo = (uint32_t)wr_row * row_bytes + 4u * wr_q;
+      if constexpr (WPT == 2) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(rw, (int)wo, (int)(k0 * BITS / 8), 0);
+        wv[0] = v[0];
+        wv[1] = v[1];
       } else {
-        fold(d, xsm, sb);
+  #pragma unroll
+        for (int h = 0; h < WPT / 4; h++) {
+          const u32x4_t v = buf_load128(rw, wo + 16u * h, k0 * BITS / 8);
+          wv[4 * h] = v.x;
+          wv[4 * h + 1] = v.y;
+          wv[4 * h + 2] = v.z;
+          wv[4 * h + 3] = v.w;
+        }
       }
-    }
-  };
-
-#pragma unroll
-  for (int p = 0; p < PF; p++) load(kb + p, xr[p], wr[p], sr[p], br[p]);
-  stash(xr[0], wr[0], sr[0], br[0], kb, 0);
-  lds_barrier();
-  // Loads are unconditional (steps past the end re-read the last one) so the
-  // count of loads between any two points is static and the waits before a
-  // stash leave the later slots in flight.
-  for (int k0 = kb; k0 < ke; k0 += PF) {
-#pragma unroll
-    for (int j = 0; j < PF; j++) {
-      const int kt = k0 + j;
-      load(kt + PF, xr[j], wr[j], sr[j], br[j]);  // slot j was staged for step kt
-      if (kt < ke) {  // workgroup-uniform
-        const int buf = (kt - kb) & 1;
-        compute(buf);
-        if (kt + 1 < ke)
-          stash(xr[(j + 1) % PF], wr[(j + 1) % PF], sr[(j + 1) % PF], br[(j + 1) % PF], kt + 1, buf ^ 1);
-        lds_barrier();
+      const uint32_t so = sb_act ? (uint32_t)(2 * sb_elem(kt)) & ~3u : OOB;
+      sv = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)so, 0, 0);
+      bv = __builtin_amdgcn_raw_buffer_load_b32(rb, (int)so, 0, 0);
+    };
+    auto stash = [&](const u32x4_t (&xv)[XL], const uint32_t (&wv)[WPT], uint32_t sv, uint32_t bv, int kt,
+                     int buf) {
+  #pragma unroll
+      for (int i = 0; i < XL; i++) {
+        const int c = tid + 256 * i, row = c / 8, unit = c % 8;
+        *reinterpret_cast<u32x4_t*>(&xs[buf][row * PITCH + 8 * unit]) = permute8<CO::ORDER>(xv[i]);
       }
+      const uint32_t magic = opaque(Mma<T>::MAGIC);
+  #pragma unroll
+      for (int u = 0; u < UPT; u++) {
+        u32x4_t op;
+        if constexpr (BITS == 4)
+          op = CodeOps<T, 4>::operand(wv[u], magic);
+        else
+          op = CodeOps<T, BITS>::operand(wv[2 * u], wv[2 * u + 1]);
+        *reinterpret_cast<u32x4_t*>(&wc[buf][wr_row * PITCH + 8 * (wr_q / UW + u)]) = op;
+      }
+      if (sb_act) {
+        const int sh = 16 * (int)(sb_elem(kt) & 1);
+        const float sc = Conv<T>::from_bits((sv >> sh) & 0xffffu), bi = Conv<T>::from_bits((bv >> sh) & 0xffffu);
+        sbl[buf][sb_e][sb_row] = make_float2(sc, bi - OFF * sc);
+      }
+    };
+
+    f32x16_t acc[TM][TN];
+  #pragma unroll
+    for (int i = 0; i < TM; i++)
+  #pragma unroll
+      for (int j = 0; j < TN; j++)
+  #pragma unroll
+        for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
+
+    const int lr = lane & 31, lh = lane >> 5;
+    const u32x4_t ones = {Mma<T>::ONES, Mma<T>::ONES, Mma<T>::ONES, Mma<T>::ONES};
+    // A group part's fold is deferred until the next part's MFMAs are issued
+    // (where registers allow), so its VALU work overlaps the matrix core; the
+    // pending part starts as zeros (folding it adds nothing).
+    constexpr bool DEFER = TM * TN <= 2;
+    f32x16_t pd[DEFER ? TM : 1][DEFER ? TN : 1], px[DEFER ? TM : 1];
+    float2 psb[DEFER ? TN : 1];
+  #pragma unroll
+    for (int i = 0; i < (DEFER ? TM : 1); i++) {
+  #pragma unroll
+      for (int v = 0; v < 16; v++) px[i][v] = 0.f;
+  #pragma unroll
+      for (int j = 0; j < (DEFER ? TN : 1); j++)
+  #pragma unroll
+        for (int v = 0; v < 16; v++) pd[i][j][v] = 0.f;
     }
-  }
+  #pragma unroll
+    for (int j = 0; j < (DEFER ? TN : 1); j++) psb[j] = make_float2(0.f, 0.f);
+    auto fold = [&](const f32x16_t (&d)[TM][TN], const f32x16_t (&xsm)[TM], const float2 (&sb)[TN]) {
+  #pragma unroll
+      for (int i = 0; i < TM; i++)
+  #pragma unroll
+        for (int j = 0; j < TN; j++)
+  #pragma unroll
+          for (int v = 0; v < 16; v++)
+            acc[i][j][v] = __builtin_fmaf(sb[j].x, d[i][j][v], __builtin_fmaf(sb[j].y, xsm[i][v], acc[i][j][v]));
+    };
+    auto compute = [&](int buf) {
+  #pragma unroll
+      for (int e = 0; e < NGK; e++) {
+        f32x16_t d[TM][TN], xsm[TM];
+  #pragma unroll
+        for (int ss = 0; ss < SPG; ss++) {
+          const int kk = 16 * (e * SPG + ss) + 8 * lh;
+          u32x4_t a[TM], b[TN];
+  #pragma unroll
+          for (int i = 0; i < TM; i++)
+            a[i] = *reinterpret_cast<const u32x4_t*>(&xs[buf][(wm * WM + 32 * i + lr) * PITCH + kk]);
+  #pragma unroll
+          for (int j = 0; j < TN; j++)
+            b[j] = *reinterpret_cast<const u32x4_t*>(&wc[buf][(wn * WN + 32 * j + lr) * PITCH + kk]);
+          f32x16_t z;
+  #pragma unroll
+          for (int v = 0; v < 16; v++) z[v] = 0.f;
+  #pragma unroll
+          for (int i = 0; i < TM; i++) {
+            xsm[i] = mma32<T>(a[i], ones, ss == 0 ? z : xsm[i]);
+  #pragma unroll
+            for (int j = 0; j < TN; j++) d[i][j] = mma32<T>(a[i], b[j], ss == 0 ? z : d[i][j]);
+          }
+        }
+        // fold: lane column n = wn WN + 32 j + lr, rows 8 (v/4) + 4 lh + v%4
+        float2 sb[TN];
+  #pragma unroll
+        for (int j = 0; j < TN; j++) sb[j] = sbl[buf][e][wn * WN + 32 * j + lr];
+        if constexpr (DEFER) {
+          fold(pd, px, psb);
+  #pragma unroll
+          for (int i = 0; i < TM; i++) {
+            px[i] = xsm[i];
+  #pragma unroll
+            for (int j = 0; j < TN; j++) pd[i][j] = d[i][j];
+          }
+  #pragma unroll
+          for (int j = 0; j < TN; j++) psb[j] = sb[j];
+        } else {
+          fold(d, xsm, sb);
+        }
+      }
+    };
 
-  if constexpr (DEFER) fold(pd, px, psb);
-
-  // D[32 x 32]: lane holds column lane % 32, rows 8 (v / 4) + 4 (lane / 32) + v % 4
-#pragma unroll
-  for (int i = 0; i < TM; i++)
-#pragma unroll
-    for (int j = 0; j < TN; j++) {
-      const int n = n0 + wn * WN + 32 * j + lr;
-#pragma unroll
-      for (int v = 0; v < 16; v++) {
-        const int m = m0 + wm * WM + 32 * i + 8 * (v / 4) + 4 * lh + v % 4;
-        if (m < Mi && n < N) {
-          if constexpr (SEG)
-            y[(yrow0 + m) * N + n] = (uint16_t)Conv<T>::to_bits(acc[i][j][v]);
-          else if (KS == 1)
-            y[((int64_t)bidx * M + m) * N + n] = (uint16_t)Conv<T>::to_bits(acc[i][j][v]);
-          else
-            part[(((int64_t)split * gridDim.z / KS + bidx) * M + m) * N + n] = acc[i][j][v];
+  #pragma unroll
+    for (int p = 0; p < PF; p++) load(kb + p, xr[p], wr[p], sr[p], br[p]);
+    stash(xr[0], wr[0], sr[0], br[0], kb, 0);
+    lds_barrier();
+    // Loads are unconditional (steps past the end re-read the last one) so the
+    // count of loads between any two points is static and the waits before a
+    // stash leave the later slots in flight.
+    for (int k0 = kb; k0 < ke; k0 += PF) {
+  #pragma unroll
+      for (int j = 0; j < PF; j++) {
+        const int kt = k0 + j;
+        load(kt + PF, xr[j], wr[j], sr[j], br[j]);  // slot j was staged for step kt
+        if (kt < ke) {  // workgroup-uniform
+          const int buf = (kt - kb) & 1;
+          compute(buf);
+          if (kt + 1 < ke)
+            stash(xr[(j + 1) % PF], wr[(j + 1) % PF], sr[(j + 1) % PF], br[(j + 1) % PF], kt + 1, buf ^ 1);
+          lds_barrier();
         }
       }
     }
+
+    if constexpr (DEFER) fold(pd, px, psb);
+
+    // D[32 x 32]: lane holds column lane % 32, rows 8 (v / 4) + 4 (lane / 32) + v % 4
+  #pragma unroll
+    for (int i = 0; i < TM; i++)
+  #pragma unroll
+      for (int j = 0; j < TN; j++) {
+        const int n = n0 + wn * WN + 32 * j + lr;
+  #pragma unroll
+        for (int v = 0; v < 16; v++) {
+          const int m = m0 + wm * WM + 32 * i + 8 * (v / 4) + 4 * lh + v % 4;
+          if (m < Mi && n < N) {
+            if constexpr (SEG)
+              y[(yrow0 + m) * N + n] = (uint16_t)Conv<T>::to_bits(acc[i][j][v]);
+            else if (KS == 1)
+              y[((int64_t)bidx * M + m) * N + n] = (uint16_t)Conv<T>::to_bits(acc[i][j][v]);
+            else
+              part[(((int64_t)split * gridDim.z / KS + bidx) * M + m) * N + n] = acc[i][j][v];
+          }
+        }
+      }
   }  // work items
 }
 
@@ -1029,8 +1030,8 @@ int launch_qmm_sorted_inst(const void* x, int64_t R, int64_t K, const uint32_t* 
   const int64_t slots = std::min<int64_t>(std::min<int64_t>(R, (R + BM - 1) / BM + n_experts), 65535);
   BatchMap bm{nullptr, idx, R, n_experts, 1, seg};
   dim3 grid((unsigned)((N + 127) / 128), 1, (unsigned)slots);
-  hipLaunchKernelGGL((qmm_tile_kernel<T, BITS, GS, BM, 128, true>), grid, dim3(256), 0, s, (const uint16_t*)x, 1, (int)K,
-                     w, (const uint16_t*)scales, (const uint16_t*)biases, (int)N, bm, 1, (int)(K / 64),
+  hipLaunchKernelGGL((qmm_tile_kernel<T, BITS, GS, BM, 128, true>), grid, dim3(256), 0, s, (const uint16_t*)x, 1,
+                     (int)K, w, (const uint16_t*)scales, (const uint16_t*)biases, (int)N, bm, 1, (int)(K / 64),
                      (uint32_t)(((n_experts * N * (K / GS)) * 2 + 3) & ~(int64_t)3), (uint16_t*)y, nullptr);
   MLXQ_LAUNCHED("qmm_tile_kernel");
   return MLXQ_OK;
