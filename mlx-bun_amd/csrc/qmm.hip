@@ -597,26 +597,32 @@ __global__ void __launch_bounds__(256) qmm_tile_kernel(const uint16_t* __restric
 // Work list of mx.gather_qmm over sorted rows: rows with equal consecutive
 // indices form one expert's run, cut into blocks of at most BM (<= 128)
 // rows; item j = (first row, rows, expert) at seg[1 + 3j], the count at
-// seg[0] (at most R items).  One workgroup walks the rows 1024 at a time,
-// each chunk's indices (and BM after it) staged in LDS: a max-scan of run
+// seg[0] (at most R items).  One workgroup stages up to 16384 indices (and
+// BM after them) in LDS with every load in flight at once, then walks them
+// 1024 rows at a time: a max-scan of run
 // starts gives each row's run start, a sum-scan numbers the block starts
 // (lane shuffles within a wave, then the 16 wave totals).  Unsorted indices
 // only give shorter runs (every row still lands in one item).
 __global__ void __launch_bounds__(1024) qmm_segments_kernel(const uint32_t* __restrict__ idx, int R, int BM,
                                                             int32_t* __restrict__ seg) {
-  __shared__ uint32_t sidx[1024 + 128];
+  constexpr int STAGE = 16384;  // rows staged per load phase (all loads of a phase in flight at once)
+  __shared__ uint32_t sidx[STAGE + 128];
   __shared__ int wmax[16], wsum[16];
   __shared__ int carry_start, carry_count;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   if (tid == 0) carry_start = 0, carry_count = 0;
-  for (int base = 0; base < R; base += 1024) {
-    for (int i = tid; i < 1024 + BM; i += 1024) sidx[i] = base + i < R ? idx[base + i] : 0u;
+  for (int base0 = 0; base0 < R; base0 += STAGE) {
+  const int nst = min(STAGE + BM, R - base0);  // every index a chunk below can read
+#pragma unroll 8
+  for (int i = tid; i < nst; i += 1024) sidx[i] = idx[base0 + i];
+  const uint32_t before0 = base0 > 0 ? idx[base0 - 1] : 0u;
+  __syncthreads();
+  for (int cb = 0; cb < STAGE && base0 + cb < R; cb += 1024) {
+    const int base = base0 + cb, loc = cb + tid;
     const int r = base + tid;
     const bool valid = r < R;
-    const uint32_t before = base > 0 ? idx[base - 1] : 0u;
-    __syncthreads();
-    const uint32_t cur = sidx[tid];
-    const bool st = valid && (r == 0 || (tid > 0 ? sidx[tid - 1] : before) != cur);
+    const uint32_t cur = sidx[loc];
+    const bool st = valid && (r == 0 || (loc > 0 ? sidx[loc - 1] : before0) != cur);
     int v = st ? r : -1;  // inclusive max-scan: latest run start at or before r
     int c;
 #pragma unroll
@@ -641,7 +647,7 @@ __global__ void __launch_bounds__(1024) qmm_segments_kernel(const uint32_t* __re
     if (f) {
       const int pos = carry_count + c - 1;
       int n = 1;
-      while (n < BM && r + n < R && sidx[tid + n] == cur) n++;
+      while (n < BM && r + n < R && sidx[loc + n] == cur) n++;
       seg[1 + 3 * pos] = r;
       seg[2 + 3 * pos] = n;
       seg[3 + 3 * pos] = (int32_t)cur;
@@ -650,13 +656,14 @@ __global__ void __launch_bounds__(1024) qmm_segments_kernel(const uint32_t* __re
     int total = 0;
     if (tid == last)
       for (int w = 0; w < 16; w++) total += wsum[w];
-    __syncthreads();  // every thread is done with carry_*, wmax, wsum and sidx
+    __syncthreads();  // every thread is done with carry_*, wmax and wsum
     if (tid == last) {
       carry_start = rs;
       carry_count += total;
     }
     __syncthreads();
   }
+  }  // load phases (the last chunk's barrier also covers the reads of sidx)
   if (tid == 0) seg[0] = carry_count;
 }
 
