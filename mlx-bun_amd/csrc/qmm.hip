@@ -604,7 +604,7 @@ __global__ void __launch_bounds__(256) qmm_tile_kernel(const uint16_t* __restric
 // (lane shuffles within a wave, then the 16 wave totals).  Unsorted indices
 // only give shorter runs (every row still lands in one item).
 __global__ void __launch_bounds__(1024) qmm_segments_kernel(const uint32_t* __restrict__ idx, int R, int BM,
-                                                            int32_t* __restrict__ seg) {
+                                                            int32_t* seg) {
   constexpr int STAGE = 16384;  // rows staged per load phase (all loads of a phase in flight at once)
   __shared__ uint32_t sidx[STAGE + 128];
   __shared__ int wmax[16], wsum[16];
@@ -644,12 +644,9 @@ __global__ void __launch_bounds__(1024) qmm_segments_kernel(const uint32_t* __re
     if (lane == 63) wsum[wave] = c;
     __syncthreads();
     for (int w = 0; w < wave; w++) c += wsum[w];
-    if (f) {
+    if (f) {  // rows of the item: set below from the next item's start
       const int pos = carry_count + c - 1;
-      int n = 1;
-      while (n < BM && r + n < R && sidx[loc + n] == cur) n++;
       seg[1 + 3 * pos] = r;
-      seg[2 + 3 * pos] = n;
       seg[3 + 3 * pos] = (int32_t)cur;
     }
     const int last = min(R - base, 1024) - 1;  // this chunk's last valid row
@@ -664,7 +661,14 @@ __global__ void __launch_bounds__(1024) qmm_segments_kernel(const uint32_t* __re
     __syncthreads();
   }
   }  // load phases (the last chunk's barrier also covers the reads of sidx)
-  if (tid == 0) seg[0] = carry_count;
+  // Every run start is a block start, so the items tile the rows in order:
+  // an item ends where the next one starts (the workgroup's own global
+  // writes are visible to it after the barrier).
+  __threadfence_block();
+  __syncthreads();
+  const int count = carry_count;
+  for (int j = tid; j < count; j += 1024) seg[2 + 3 * j] = (j + 1 < count ? seg[1 + 3 * (j + 1)] : R) - seg[1 + 3 * j];
+  if (tid == 0) seg[0] = count;
 }
 
 // y = T(sum over splits of the fp32 partials), fixed split order.
