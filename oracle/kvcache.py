@@ -1,4 +1,4 @@
-"""Restatement of the reference's quantized KV caches over numpy arrays.
+"""Restatement of the reference's KV caches over numpy arrays.
 
 TEST INFRASTRUCTURE ONLY (the checker for the device caches in the mlxq
 package).  Pure bookkeeping around ``oracle.quantize``: growth, ring writes,
@@ -6,6 +6,11 @@ temporal reordering and trimming, step for step as
 src/model/gemma4-base.ts:419-600 (QuantizedKVCache) and :932-1260
 (RotatingQuantizedKVCache) do them.  A triple is (packed, scales, biases)
 with shapes [B, H, S, D*bits/32], [B, H, S, D/gs] x 2 (T bit patterns).
+
+The T-typed caches (KVCache :254-405, RotatingKVCache :604-910; values held
+as float32 arrays of T values), their toQuantized conversions (:393-404,
+:887-903) and maybeQuantizeKv (src/generate.ts:101-129) are restated below
+the quantized ones.
 """
 from __future__ import annotations
 
@@ -150,3 +155,151 @@ class RotatingQuantizedKVCache:
         if k.shape[2] == 1:
             return self._update_in_place(k, v, dtype)
         return self._update_concat(k, v, dtype)
+
+
+# ------------------------------------------------------------ T-typed caches
+
+class KVCache:
+    """gemma4-base.ts:254-324: capacity grows by whole STEP=256 blocks; when
+    `offset` is not a multiple of STEP the buffer is first cut back to it."""
+
+    STEP = 256
+
+    def __init__(self):
+        self.keys = self.values = None
+        self.offset = 0
+
+    def update_and_fetch(self, k, v):
+        prev = self.offset
+        B, H, L, D = k.shape
+        vD = v.shape[3]
+        if self.keys is None or prev + L > self.keys.shape[2]:
+            n = ((self.STEP + L - 1) // self.STEP) * self.STEP
+            zk = np.zeros((B, H, n, D), np.float32)
+            zv = np.zeros((B, H, n, vD), np.float32)
+            if self.keys is None:
+                self.keys, self.values = zk, zv
+            else:
+                ok, ov = self.keys, self.values
+                if prev % self.STEP != 0:
+                    ok, ov = ok[:, :, :prev], ov[:, :, :prev]
+                self.keys = np.concatenate([ok, zk], 2)
+                self.values = np.concatenate([ov, zv], 2)
+        self.offset += L
+        self.keys[:, :, prev:self.offset] = k
+        self.values[:, :, prev:self.offset] = v
+        return self.keys[:, :, :self.offset], self.values[:, :, :self.offset]
+
+    def to_quantized(self, gs, bits, dtype):
+        """:393-404 -- the whole buffer (padding included), offset kept."""
+        q = QuantizedKVCache(gs, bits)
+        q.offset = self.offset
+        if self.keys is not None:
+            q.keys = O.quantize(self.keys, gs, bits, dtype)
+            q.values = O.quantize(self.values, gs, bits, dtype)
+        return q
+
+
+class RotatingKVCache:
+    """gemma4-base.ts:604-910 with keep=0: the ring mechanics of
+    RotatingQuantizedKVCache over T values."""
+
+    STEP = 256
+
+    def __init__(self, max_size: int):
+        self.max_size = max_size
+        self.keys = self.values = None
+        self.offset = 0
+        self.ring_idx = 0
+
+    def _seq_len(self):
+        return 0 if self.keys is None else self.keys.shape[2]
+
+    def _temporal(self, a):
+        S = a.shape[2]
+        if self.ring_idx == S:
+            return a[:, :, :S].copy()
+        if self.ring_idx < self.offset:
+            return np.concatenate([a[:, :, self.ring_idx:], a[:, :, :self.ring_idx]], 2)
+        return a[:, :, :self.ring_idx].copy()
+
+    def _update_concat(self, k, v):
+        S = k.shape[2]
+        if self.keys is None:
+            self.keys, self.values = k.copy(), v.copy()
+        else:
+            tk, tv = self._temporal(self.keys), self._temporal(self.values)
+            self.ring_idx = tk.shape[2]
+            trim = max(self.ring_idx - self.max_size + 1, 0)
+            self.keys = np.concatenate([tk[:, :, trim:], k], 2)
+            self.values = np.concatenate([tv[:, :, trim:], v], 2)
+        self.offset += S
+        self.ring_idx = self._seq_len()
+        return self.keys, self.values
+
+    def _update_in_place(self, k, v):
+        B, H, S, D = k.shape
+        vD = v.shape[3]
+        prev = self.offset
+        if self.keys is None or (prev >= self._seq_len() and self._seq_len() < self.max_size):
+            n = min(self.STEP, self.max_size - prev)
+            zk = np.zeros((B, H, n, D), np.float32)
+            zv = np.zeros((B, H, n, vD), np.float32)
+            if self.keys is None:
+                self.keys, self.values = zk, zv
+            else:
+                self.keys = np.concatenate([self.keys, zk], 2)
+                self.values = np.concatenate([self.values, zv], 2)
+            self.ring_idx = prev
+        trim = self._seq_len() - self.max_size
+        if trim > 0:
+            self.keys = self.keys[:, :, trim:].copy()
+            self.values = self.values[:, :, trim:].copy()
+            self.ring_idx = self.max_size
+        if self.ring_idx == self.max_size:
+            self.ring_idx = 0
+        self.keys[:, :, self.ring_idx:self.ring_idx + S] = k
+        self.values[:, :, self.ring_idx:self.ring_idx + S] = v
+        self.offset += S
+        self.ring_idx += S
+        if self.offset < self.max_size:
+            return self.keys[:, :, :self.offset], self.values[:, :, :self.offset]
+        return self.keys, self.values
+
+    def update_and_fetch(self, k, v):
+        if k.shape[2] == 1:
+            return self._update_in_place(k, v)
+        return self._update_concat(k, v)
+
+    def to_quantized(self, gs, bits, dtype):
+        """:887-903 -- quantized as laid out (ring order); offset and ring
+        index kept."""
+        q = RotatingQuantizedKVCache(self.max_size, gs, bits)
+        if self.keys is not None:
+            q.keys = O.quantize(self.keys, gs, bits, dtype)
+            q.values = O.quantize(self.values, gs, bits, dtype)
+        q.offset = self.offset
+        q.ring_idx = self.ring_idx
+        return q
+
+
+def maybe_quantize_kv(cache, dtype, kv_bits=None, kv_group_size=None, kv_config=None, quantized_kv_start=None):
+    """src/generate.ts:101-129: convert T caches whose offset reached the
+    start (default 0 with a per-layer config, else 5000), skipping empty
+    ones; a config {layer: (bits, group_size)} converts only the layers it
+    names.  Returns the new list."""
+    if not kv_bits and not kv_config:
+        return list(cache)
+    start = quantized_kv_start if quantized_kv_start is not None else (0 if kv_config else 5000)
+    out = list(cache)
+    for i, c in enumerate(cache):
+        if not isinstance(c, (KVCache, RotatingKVCache)) or c.offset < start or c.offset == 0:
+            continue
+        if kv_config:
+            if i not in kv_config:
+                continue
+            bits, gs = kv_config[i]
+        else:
+            bits, gs = kv_bits, (kv_group_size if kv_group_size is not None else 64)
+        out[i] = c.to_quantized(gs, bits, dtype)
+    return out
