@@ -93,13 +93,25 @@ int mlxq_event_record(void* event, void* stream);
 int mlxq_event_elapsed_ms(void* start, void* stop, float* ms);
 /* HIP graph capture of the calls issued on `stream` between begin and end
  * (the analogue of the reference's compiled decode closures,
- * src/model/compiled-decode.ts, for launch-bound loops).  Library calls
- * that would allocate workspace fail while capturing: run them once before
- * capture. */
+ * src/model/compiled-decode.ts, for launch-bound loops).
+ * Workspace: decode split-K partials, the qmm split-K partials and the
+ * sorted gather's work list live in one library-owned block per device.  A
+ * call that needs the block to grow fails (MLXQ_ERR_STATE) while its stream
+ * is being captured: run the call once, or reserve, before capture.  While
+ * any exec made by mlxq_graph_end exists, a later eager call that grows the
+ * block leaves the old one allocated (a replay keeps reading and writing
+ * it); replaced blocks are freed when the last such exec is destroyed.
+ * Graphs captured by other means are not tracked: reserve enough before
+ * capturing them.  Replays and calls that overlap on one device race on the
+ * block (serialise them on one stream). */
 int mlxq_graph_begin(void* stream);
 int mlxq_graph_end(void* stream, void** graph_exec);
 int mlxq_graph_launch(void* graph_exec, void* stream);
 int mlxq_graph_destroy(void* graph_exec);
+/* Grow the current device's workspace to at least `nbytes` now (not while
+ * `stream` is being captured); its current size. */
+int mlxq_workspace_reserve(uint64_t nbytes, void* stream);
+int mlxq_workspace_size(uint64_t* nbytes);
 
 /* -------------------------------------------------------------- quantize */
 

@@ -43,16 +43,22 @@ int device_cu_count();
     if (e_ != hipSuccess) return ::mlxq::hip_fail(e_, name);  \
   } while (0)
 
-// Per-device scratch owned by the library: a fixed block of arrival
-// counters (zeroed at allocation; every kernel that increments one resets it
-// before exiting) followed by a growable region for split-K partials.  Calls
-// that overlap on one device race on it.
-constexpr size_t kMaxCounters = 65536;
-struct Workspace {
-  void* ptr = nullptr;
-  size_t bytes = 0;
+// Per-device workspace owned by the library (split-K partials, work lists):
+// one growable block per device, handed to every call that needs scratch.
+// Calls that overlap on one device race on it.  A block that a captured
+// graph may still reference is never freed while such a graph exists
+// (retired blocks are freed once the last mlxq_graph_* exec is destroyed),
+// and the block cannot grow while the stream is being captured.
+int workspace(size_t bytes, void** out, hipStream_t stream);
+
+// Where a call's scratch comes from: the growable workspace above, or a
+// fixed block, which a request larger than `fixed_bytes` fails against
+// instead of growing.
+struct Scratch {
+  void* fixed = nullptr;
+  size_t fixed_bytes = 0;
+  int get(size_t bytes, void** out, hipStream_t stream) const;
 };
-int workspace(size_t partial_bytes, size_t ncounters, uint32_t** counters, void** partial, hipStream_t stream);
 
 inline bool is_half_dtype(int dtype) { return dtype == MLXQ_FLOAT16 || dtype == MLXQ_BFLOAT16; }
 inline bool dtype_supported(int dtype) { return is_half_dtype(dtype) || dtype == MLXQ_FLOAT32; }

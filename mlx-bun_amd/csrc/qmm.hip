@@ -723,9 +723,8 @@ int launch_qmm_tile_inst(const void* x, int64_t batch, int64_t M, int64_t K, con
   const size_t pbytes = KS > 1 ? (size_t)KS * batch * M * N * sizeof(float) : 0;
   float* part = nullptr;
   if (pbytes) {
-    uint32_t* unused_counters = nullptr;
     void* p = nullptr;
-    int rc = mlxq::workspace(pbytes, 0, &unused_counters, &p, s);
+    int rc = mlxq::workspace(pbytes, &p, s);
     if (rc) return rc;
     part = (float*)p;
   }
@@ -1030,8 +1029,7 @@ int launch_qmm_sorted_inst(const void* x, int64_t R, int64_t K, const uint32_t* 
                            hipStream_t s) {
   static_assert(BM <= 128, "qmm_segments_kernel stages BM indices past each chunk");
   void* p = nullptr;
-  uint32_t* unused_counters = nullptr;
-  int rc = mlxq::workspace((1 + 3 * (size_t)R) * sizeof(int32_t), 0, &unused_counters, &p, s);
+  int rc = mlxq::workspace((1 + 3 * (size_t)R) * sizeof(int32_t), &p, s);
   if (rc) return rc;
   int32_t* seg = (int32_t*)p;
   hipLaunchKernelGGL(qmm_segments_kernel, dim3(1), dim3(1024), 0, s, idx, (int)R, BM, seg);

@@ -17,7 +17,16 @@ static std::mutex g_mu;
 static int g_device = -1;
 static hipStream_t g_stream = nullptr;
 static int g_cu_count = 0;
-static std::vector<Workspace> g_ws;  // indexed by device
+
+// Per-device workspace: the live block and the blocks it replaced that a
+// captured graph may still reference.
+struct DeviceWorkspace {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+  std::vector<void*> retired;
+};
+static std::vector<DeviceWorkspace> g_ws;  // indexed by device
+static int g_live_graphs = 0;              // graph execs made by mlxq_graph_end, not yet destroyed
 
 void set_error(const std::string& msg) { g_last_error = msg; }
 
@@ -37,30 +46,62 @@ hipStream_t resolve_stream(void* s) { return s ? (hipStream_t)s : g_stream; }
 
 int device_cu_count() { return g_cu_count; }
 
-int workspace(size_t partial_bytes, size_t ncounters, uint32_t** counters, void** partial, hipStream_t stream) {
-  if (ncounters > kMaxCounters) return fail(MLXQ_ERR_UNSUPPORTED, "workspace: too many split-K counters");
-  const size_t cbytes = kMaxCounters * sizeof(uint32_t);
-  const size_t bytes = cbytes + partial_bytes;
-  std::lock_guard<std::mutex> lk(g_mu);
+// Grows the current device's block to at least `bytes` (caller holds g_mu).
+static int grow_locked(size_t bytes, hipStream_t stream) {
   int dev = 0;
   MLXQ_HIP(hipGetDevice(&dev));
   if ((int)g_ws.size() <= dev) g_ws.resize(dev + 1);
-  Workspace& w = g_ws[dev];
-  if (w.bytes < bytes) {
-    size_t nb = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
-    nb = (nb + 4095) & ~(size_t)4095;
-    if (w.ptr) {
+  DeviceWorkspace& w = g_ws[dev];
+  if (w.bytes >= bytes) return MLXQ_OK;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  MLXQ_HIP(hipStreamIsCapturing(stream, &cs));
+  if (cs != hipStreamCaptureStatusNone)
+    return fail(MLXQ_ERR_STATE, "the library workspace must grow to " + std::to_string(bytes) +
+                                    " bytes while the stream is being captured: run the call once, or "
+                                    "mlxq_workspace_reserve, before capture");
+  size_t nb = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
+  nb = (nb + 4095) & ~(size_t)4095;
+  void* p = nullptr;
+  MLXQ_HIP(hipMalloc(&p, nb));
+  if (w.ptr) {
+    if (g_live_graphs > 0) {
+      w.retired.push_back(w.ptr);  // a replay may still read or write it
+    } else {
       MLXQ_HIP(hipStreamSynchronize(stream));
       MLXQ_HIP(hipFree(w.ptr));
-      w.ptr = nullptr;
-      w.bytes = 0;
     }
-    MLXQ_HIP(hipMalloc(&w.ptr, nb));
-    MLXQ_HIP(hipMemset(w.ptr, 0, nb));
-    w.bytes = nb;
   }
-  *counters = reinterpret_cast<uint32_t*>(w.ptr);
-  *partial = reinterpret_cast<uint8_t*>(w.ptr) + cbytes;
+  w.ptr = p;
+  w.bytes = nb;
+  return MLXQ_OK;
+}
+
+int workspace(size_t bytes, void** out, hipStream_t stream) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  int rc = grow_locked(bytes, stream);
+  if (rc) return rc;
+  int dev = 0;
+  MLXQ_HIP(hipGetDevice(&dev));
+  *out = g_ws[dev].ptr;
+  return MLXQ_OK;
+}
+
+int Scratch::get(size_t bytes, void** out, hipStream_t stream) const {
+  if (!fixed) return workspace(bytes, out, stream);
+  if (bytes > fixed_bytes)
+    return fail(MLXQ_ERR_UNSUPPORTED, "this call needs " + std::to_string(bytes) + " bytes of scratch, more than the " +
+                                          std::to_string(fixed_bytes) + "-byte fixed block");
+  *out = fixed;
+  return MLXQ_OK;
+}
+
+// Frees every retired block once no graph exec can reference one.
+static int release_retired_locked() {
+  if (g_live_graphs > 0) return MLXQ_OK;
+  for (DeviceWorkspace& w : g_ws) {
+    for (void* p : w.retired) MLXQ_HIP(hipFree(p));
+    w.retired.clear();
+  }
   return MLXQ_OK;
 }
 
@@ -230,6 +271,8 @@ int mlxq_graph_end(void* stream, void** graph_exec) {
   (void)hipGraphDestroy(g);
   if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
   *graph_exec = ge;
+  std::lock_guard<std::mutex> lk(g_mu);
+  ++g_live_graphs;
   return MLXQ_OK;
 }
 
@@ -241,7 +284,26 @@ int mlxq_graph_launch(void* graph_exec, void* stream) {
 
 int mlxq_graph_destroy(void* graph_exec) {
   MLXQ_REQUIRE_INIT();
-  if (graph_exec) MLXQ_HIP(hipGraphExecDestroy((hipGraphExec_t)graph_exec));
+  if (!graph_exec) return MLXQ_OK;
+  MLXQ_HIP(hipGraphExecDestroy((hipGraphExec_t)graph_exec));
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (g_live_graphs > 0) --g_live_graphs;
+  return release_retired_locked();
+}
+
+int mlxq_workspace_reserve(uint64_t nbytes, void* stream) {
+  MLXQ_REQUIRE_INIT();
+  std::lock_guard<std::mutex> lk(g_mu);
+  return grow_locked((size_t)nbytes, resolve_stream(stream));
+}
+
+int mlxq_workspace_size(uint64_t* nbytes) {
+  MLXQ_REQUIRE_INIT();
+  if (!nbytes) return fail(MLXQ_ERR_ARGUMENT, "null out-pointer");
+  int dev = 0;
+  MLXQ_HIP(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lk(g_mu);
+  *nbytes = dev < (int)g_ws.size() ? g_ws[dev].bytes : 0;
   return MLXQ_OK;
 }
 

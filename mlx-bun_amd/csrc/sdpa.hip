@@ -17,8 +17,9 @@
 //             the score layout of lane l (column l%16, keys 4*(l/16)+i and
 //             16+4*(l/16)+i) is exactly the A operand layout, so p never
 //             moves between lanes.
-// Waves merge through LDS; chunks of one (b, kv head) merge in the last
-// workgroup to arrive (fixed order, deterministic).  Key chunk geometry
+// Waves merge through LDS; the chunks of one (b, kv head) write fp32
+// partials (U, M, L) that a second kernel, sdpa_decode_merge_kernel, merges
+// in fixed chunk order (deterministic, no atomics).  Key chunk geometry
 // handles the rotating caches' ring (slot = (ring_off - valid + j) mod cap).
 //
 // Everything the MFMA decode kernel does not cover (Lq > 1, D = 512 or
@@ -1822,7 +1823,8 @@ __global__ void __launch_bounds__(256) sdpa_prefill_wide_kernel(
 template <typename T, int BITS>
 int launch_prefill_wide(int D, int gs, const void* q, int B, int Hq, int Hkv, int Lq, const uint32_t* kp,
                         const void* ks, const void* kb, const uint32_t* vp, const void* vs, const void* vb,
-                        Geometry geo, int causal, int window, float scale, void* out, hipStream_t s) {
+                        Geometry geo, int causal, int window, float scale, void* out, hipStream_t s,
+                        const mlxq::Scratch& scr) {
   const int nrep = Hq / Hkv;
   const int64_t rows = (int64_t)Lq * nrep;
   // Fewer row blocks than CUs (one 4-wave workgroup fills a CU): split each
@@ -1842,8 +1844,7 @@ int launch_prefill_wide(int D, int gs, const void* q, int B, int Hq, int Hkv, in
     const size_t slots = (size_t)B * Hkv * nsplit;
     const size_t obytes = (slots * rows * D * sizeof(float) + 255) & ~(size_t)255;
     void* pws = nullptr;
-    uint32_t* unused_counters = nullptr;
-    int rc = mlxq::workspace(obytes + slots * rows * sizeof(float2), 0, &unused_counters, &pws, s);
+    int rc = scr.get(obytes + slots * rows * sizeof(float2), &pws, s);
     if (rc) return rc;
     part_o = (float*)pws;
     part_ml = (float2*)((uint8_t*)pws + obytes);
@@ -2012,7 +2013,7 @@ int decode_chunk_override() {
 template <typename T, int BITS, int D, int GS>
 int launch_decode(const void* q, int B, int Hq, int Hkv, const uint32_t* kp, const void* ks, const void* kb,
                   const uint32_t* vp, const void* vs, const void* vb, Geometry geo, float scale, void* out,
-                  hipStream_t s) {
+                  hipStream_t s, const mlxq::Scratch& scr) {
   using SH = DecodeShape<BITS, D, GS>;
   constexpr int MAXC = SH::MAXC;
   MLXQ_CHECK(geo.cap * (int64_t)SH::KW * 4 < ((int64_t)1 << 31), "kv cache rows too long for one launch");
@@ -2035,8 +2036,7 @@ int launch_decode(const void* q, int B, int Hq, int Hkv, const uint32_t* kp, con
   const size_t obytes = (slots * nrep * D * sizeof(float) + 255) & ~(size_t)255;
   const size_t pbytes = nchunks > 1 ? obytes + slots * nrep * sizeof(float2) : 0;
   if (pbytes) {
-    uint32_t* unused_counters = nullptr;
-    int rc = mlxq::workspace(pbytes, 0, &unused_counters, &pws, s);
+    int rc = scr.get(pbytes, &pws, s);
     if (rc) return rc;
   }
   float* part_o = (float*)pws;
@@ -2057,10 +2057,10 @@ int launch_decode(const void* q, int B, int Hq, int Hkv, const uint32_t* kp, con
 template <typename T, int BITS>
 int launch_decode_d(int D, int gs, const void* q, int B, int Hq, int Hkv, const uint32_t* kp, const void* ks,
                     const void* kb, const uint32_t* vp, const void* vs, const void* vb, Geometry geo, float scale,
-                    void* out, hipStream_t s) {
+                    void* out, hipStream_t s, const mlxq::Scratch& scr) {
 #define DEC(DV, GV)                                                                                             \
   if (D == DV && gs == GV)                                                                                      \
-    return launch_decode<T, BITS, DV, GV>(q, B, Hq, Hkv, kp, ks, kb, vp, vs, vb, geo, scale, out, s);
+    return launch_decode<T, BITS, DV, GV>(q, B, Hq, Hkv, kp, ks, kb, vp, vs, vb, geo, scale, out, s, scr);
   DEC(128, 32) DEC(128, 64) DEC(128, 128)
   DEC(256, 32) DEC(256, 64) DEC(256, 128)
   if constexpr (BITS == 8) {
@@ -2073,7 +2073,7 @@ int launch_decode_d(int D, int gs, const void* q, int B, int Hq, int Hkv, const 
 template <typename T, int BITS, int D, int GS>
 int launch_decode_wide(const void* q, int B, int Hq, int Hkv, const uint32_t* kp, const void* ks, const void* kb,
                        const uint32_t* vp, const void* vs, const void* vb, Geometry geo, float scale, void* out,
-                       hipStream_t s) {
+                       hipStream_t s, const mlxq::Scratch& scr) {
   using SH = WideShape<D, GS, BITS>;
   MLXQ_CHECK(geo.cap * (int64_t)SH::KW * 4 < ((int64_t)1 << 31), "kv cache rows too long for one launch");
   const int64_t span = geo.valid_len ? geo.cap : geo.n_kv;  // per-row upper bound on keys
@@ -2094,8 +2094,7 @@ int launch_decode_wide(const void* q, int B, int Hq, int Hkv, const uint32_t* kp
   const size_t obytes = (slots * nrep * D * sizeof(float) + 255) & ~(size_t)255;
   const size_t pbytes = nchunks > 1 ? obytes + slots * nrep * sizeof(float2) : 0;
   if (pbytes) {
-    uint32_t* unused_counters = nullptr;
-    int rc = mlxq::workspace(pbytes, 0, &unused_counters, &pws, s);
+    int rc = scr.get(pbytes, &pws, s);
     if (rc) return rc;
   }
   float* part_o = (float*)pws;
@@ -2116,10 +2115,10 @@ int launch_decode_wide(const void* q, int B, int Hq, int Hkv, const uint32_t* kp
 template <typename T, int BITS>
 int launch_decode_wide_d(int D, int gs, const void* q, int B, int Hq, int Hkv, const uint32_t* kp, const void* ks,
                          const void* kb, const uint32_t* vp, const void* vs, const void* vb, Geometry geo,
-                         float scale, void* out, hipStream_t s) {
+                         float scale, void* out, hipStream_t s, const mlxq::Scratch& scr) {
 #define WDEC(DV, GV)                                                                                            \
   if (D == DV && gs == GV)                                                                                      \
-    return launch_decode_wide<T, BITS, DV, GV>(q, B, Hq, Hkv, kp, ks, kb, vp, vs, vb, geo, scale, out, s);
+    return launch_decode_wide<T, BITS, DV, GV>(q, B, Hq, Hkv, kp, ks, kb, vp, vs, vb, geo, scale, out, s, scr);
   WDEC(128, 32) WDEC(128, 64) WDEC(128, 128)
   WDEC(256, 32) WDEC(256, 64) WDEC(256, 128)
   WDEC(512, 64) WDEC(512, 128)
@@ -2152,14 +2151,13 @@ bool decode_mfma_ok(int dtype, int bits, int D, int gs, int nrep, std::initializ
   return nrep * (D / gs) <= 16;
 }
 
-}  // namespace
-
-extern "C" int mlxq_quantized_sdpa(const void* q, int dtype, int B, int Hq, int Hkv, int Lq, int D,
-                                   const uint32_t* k_packed, const void* k_scales, const void* k_biases,
-                                   const uint32_t* v_packed, const void* v_scales, const void* v_biases,
-                                   int64_t kv_capacity, int64_t n_kv, const int32_t* valid_len,
-                                   const int32_t* ring_offset, int mask_mode, int window, float scale,
-                                   int group_size, int bits, void* out, void* stream) {
+// The whole dispatch of mlxq_quantized_sdpa, with its scratch (split-K
+// partials) taken from `scr`.
+int sdpa_dispatch(const void* q, int dtype, int B, int Hq, int Hkv, int Lq, int D, const uint32_t* k_packed,
+                  const void* k_scales, const void* k_biases, const uint32_t* v_packed, const void* v_scales,
+                  const void* v_biases, int64_t kv_capacity, int64_t n_kv, const int32_t* valid_len,
+                  const int32_t* ring_offset, int mask_mode, int window, float scale, int group_size, int bits,
+                  void* out, void* stream, const mlxq::Scratch& scr) {
   MLXQ_REQUIRE_INIT();
   MLXQ_CHECK(mlxq::dtype_supported(dtype), "dtype must be float16, bfloat16 or float32");
   MLXQ_CHECK(bits == 2 || bits == 4 || bits == 8, "bits must be 2, 4 or 8");
@@ -2184,24 +2182,24 @@ extern "C" int mlxq_quantized_sdpa(const void* q, int dtype, int B, int Hq, int 
   if (decode && decode_mfma_ok(dtype, bits, D, group_size, nrep, {k_scales, k_biases, v_scales, v_biases})) {
     if (dtype == MLXQ_BFLOAT16)
       return bits == 4 ? launch_decode_d<BF16, 4>(D, group_size, q, B, Hq, Hkv, k_packed, k_scales, k_biases,
-                                                  v_packed, v_scales, v_biases, geo, scale, out, s)
+                                                  v_packed, v_scales, v_biases, geo, scale, out, s, scr)
                        : launch_decode_d<BF16, 8>(D, group_size, q, B, Hq, Hkv, k_packed, k_scales, k_biases,
-                                                  v_packed, v_scales, v_biases, geo, scale, out, s);
+                                                  v_packed, v_scales, v_biases, geo, scale, out, s, scr);
     return bits == 4 ? launch_decode_d<F16, 4>(D, group_size, q, B, Hq, Hkv, k_packed, k_scales, k_biases, v_packed,
-                                               v_scales, v_biases, geo, scale, out, s)
+                                               v_scales, v_biases, geo, scale, out, s, scr)
                      : launch_decode_d<F16, 8>(D, group_size, q, B, Hq, Hkv, k_packed, k_scales, k_biases, v_packed,
-                                               v_scales, v_biases, geo, scale, out, s);
+                                               v_scales, v_biases, geo, scale, out, s, scr);
   }
   if (decode && decode_wide_ok(dtype, bits, D, group_size, nrep, {k_scales, k_biases, v_scales, v_biases})) {
     if (dtype == MLXQ_BFLOAT16)
       return bits == 4 ? launch_decode_wide_d<BF16, 4>(D, group_size, q, B, Hq, Hkv, k_packed, k_scales, k_biases,
-                                                       v_packed, v_scales, v_biases, geo, scale, out, s)
+                                                       v_packed, v_scales, v_biases, geo, scale, out, s, scr)
                        : launch_decode_wide_d<BF16, 8>(D, group_size, q, B, Hq, Hkv, k_packed, k_scales, k_biases,
-                                                       v_packed, v_scales, v_biases, geo, scale, out, s);
+                                                       v_packed, v_scales, v_biases, geo, scale, out, s, scr);
     return bits == 4 ? launch_decode_wide_d<F16, 4>(D, group_size, q, B, Hq, Hkv, k_packed, k_scales, k_biases,
-                                                    v_packed, v_scales, v_biases, geo, scale, out, s)
+                                                    v_packed, v_scales, v_biases, geo, scale, out, s, scr)
                      : launch_decode_wide_d<F16, 8>(D, group_size, q, B, Hq, Hkv, k_packed, k_scales, k_biases,
-                                                    v_packed, v_scales, v_biases, geo, scale, out, s);
+                                                    v_packed, v_scales, v_biases, geo, scale, out, s, scr);
   }
   const int causal = mask_mode == MLXQ_MASK_CAUSAL;
   // Lq > 1 on the matrix cores: plain (non-ring) caches, T = bf16/f16, 4/8-bit
@@ -2228,13 +2226,13 @@ extern "C" int mlxq_quantized_sdpa(const void* q, int dtype, int B, int Hq, int 
   if (prefill_wide_ok) {
     if (dtype == MLXQ_BFLOAT16)
       return bits == 4 ? launch_prefill_wide<BF16, 4>(D, group_size, q, B, Hq, Hkv, Lq, k_packed, k_scales, k_biases,
-                                                      v_packed, v_scales, v_biases, geo, causal, window, scale, out, s)
+                                                      v_packed, v_scales, v_biases, geo, causal, window, scale, out, s, scr)
                        : launch_prefill_wide<BF16, 8>(D, group_size, q, B, Hq, Hkv, Lq, k_packed, k_scales, k_biases,
-                                                      v_packed, v_scales, v_biases, geo, causal, window, scale, out, s);
+                                                      v_packed, v_scales, v_biases, geo, causal, window, scale, out, s, scr);
     return bits == 4 ? launch_prefill_wide<F16, 4>(D, group_size, q, B, Hq, Hkv, Lq, k_packed, k_scales, k_biases,
-                                                   v_packed, v_scales, v_biases, geo, causal, window, scale, out, s)
+                                                   v_packed, v_scales, v_biases, geo, causal, window, scale, out, s, scr)
                      : launch_prefill_wide<F16, 8>(D, group_size, q, B, Hq, Hkv, Lq, k_packed, k_scales, k_biases,
-                                                   v_packed, v_scales, v_biases, geo, causal, window, scale, out, s);
+                                                   v_packed, v_scales, v_biases, geo, causal, window, scale, out, s, scr);
   }
   dim3 grid((unsigned)Lq, (unsigned)Hq, (unsigned)B);
   MLXQ_DISPATCH_T(dtype, TT, {
@@ -2255,4 +2253,17 @@ extern "C" int mlxq_quantized_sdpa(const void* q, int dtype, int B, int Hq, int 
   });
   MLXQ_LAUNCHED("sdpa_generic_kernel");
   return MLXQ_OK;
+}
+
+}  // namespace
+
+extern "C" int mlxq_quantized_sdpa(const void* q, int dtype, int B, int Hq, int Hkv, int Lq, int D,
+                                   const uint32_t* k_packed, const void* k_scales, const void* k_biases,
+                                   const uint32_t* v_packed, const void* v_scales, const void* v_biases,
+                                   int64_t kv_capacity, int64_t n_kv, const int32_t* valid_len,
+                                   const int32_t* ring_offset, int mask_mode, int window, float scale,
+                                   int group_size, int bits, void* out, void* stream) {
+  return sdpa_dispatch(q, dtype, B, Hq, Hkv, Lq, D, k_packed, k_scales, k_biases, v_packed, v_scales, v_biases,
+                       kv_capacity, n_kv, valid_len, ring_offset, mask_mode, window, scale, group_size, bits, out,
+                       stream, mlxq::Scratch{});
 }

@@ -25,6 +25,7 @@ SYMBOLS = (
     "mlxq_fill_zero", "mlxq_copy_2d", "mlxq_stream_create", "mlxq_stream_destroy", "mlxq_synchronize",
     "mlxq_event_create", "mlxq_event_destroy", "mlxq_event_record", "mlxq_event_elapsed_ms",
     "mlxq_graph_begin", "mlxq_graph_end", "mlxq_graph_launch", "mlxq_graph_destroy",
+    "mlxq_workspace_reserve", "mlxq_workspace_size",
     "mlxq_quantize", "mlxq_kv_append", "mlxq_dequantize", "mlxq_embedding_gather", "mlxq_quantized_matmul",
     "mlxq_gather_qmm", "mlxq_gather_qmm_sorted",
     "mlxq_quantized_sdpa",
@@ -63,6 +64,8 @@ def _declare(L: ctypes.CDLL) -> None:
         "mlxq_graph_end": [P, P],
         "mlxq_graph_launch": [P, P],
         "mlxq_graph_destroy": [P],
+        "mlxq_workspace_reserve": [U64, P],
+        "mlxq_workspace_size": [P],
         "mlxq_quantize": [P, I, I64, I64, I, I, P, P, P, P],
         "mlxq_kv_append": [P, I, I64, I64, I64, I, I, P, P, P, I64, I64, P],
         "mlxq_dequantize": [P, P, P, I, I64, I64, I, I, P, P],

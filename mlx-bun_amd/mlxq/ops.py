@@ -193,9 +193,9 @@ def gatherQmm(x: DeviceArray, w: DeviceArray, scales: DeviceArray, biases: Optio
         _lib.call("mlxq_gather_qmm", x.ptr, x.dtype, x_batch, batch, M, K,
                   x_map.ptr if x_map is not None else None, idx.ptr, w.ptr, scales.ptr, biases.ptr, E, N,
                   spec.groupSize, spec.bits, int(bool(transpose)), y.ptr, None)
-    # the temporaries are freed (hipFree, which waits for the device) only
-    # after the launch that reads them
-    del keep
+    # the temporaries live as long as the output: the launch (or a captured
+    # graph replaying it) reads them after this returns
+    y._deps = keep
     return y
 
 
