@@ -69,6 +69,8 @@ class SafetensorsFile:
             if dtype not in _DTYPES:
                 raise ValueError(f"{path}: tensor {name} has unsupported dtype {dtype}")
             expected = int(np.prod(shape)) * _DTYPES[dtype][0] if shape else _DTYPES[dtype][0]
+            if begin < 0 or end < begin:
+                raise ValueError(f"{path}: tensor {name} has data_offsets [{begin}, {end}] out of order")
             if end - begin != expected:
                 raise ValueError(f"{path}: tensor {name} byte range {end - begin} != shape {list(shape)} x {dtype}")
             if self._data_start + end > size:
@@ -106,10 +108,14 @@ class ShardedSafetensors:
         if os.path.exists(index):
             with open(index) as f:
                 weight_map = json.load(f)["weight_map"]
+            root = os.path.realpath(model_dir)
             for tensor, file in weight_map.items():
                 sf = self.files.get(file)
                 if sf is None:
-                    sf = self.files[file] = SafetensorsFile(os.path.join(model_dir, file))
+                    path = os.path.realpath(os.path.join(model_dir, file))
+                    if os.path.commonpath([root, path]) != root:
+                        raise ValueError(f"{index}: shard {file!r} of {tensor} lies outside the model directory")
+                    sf = self.files[file] = SafetensorsFile(path)
                 self.tensor_to_file[tensor] = sf
         else:
             sf = SafetensorsFile(os.path.join(model_dir, "model.safetensors"))

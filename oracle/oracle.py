@@ -18,7 +18,7 @@ import subprocess
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "_build", "liboracle.so")
+LIB_PATH = os.environ.get("ORACLE_LIB", os.path.join(HERE, "_build", "liboracle.so"))
 
 F16, F32, BF16 = 9, 10, 12
 DTYPES = {"float16": F16, "float32": F32, "bfloat16": BF16}
@@ -228,12 +228,21 @@ def ring_slot_mask(valid: int, ring_off: int, cap: int) -> np.ndarray:
     return m
 
 
-def lcg_floats(n: int, seed: int) -> np.ndarray:
-    """The reference tests' deterministic LCG in [-1, 1)
-    (tests/fused-sdpa.test.ts:29-38)."""
+def lcg_floats(n: int, seed: int, divisor: float = 2 ** 32) -> np.ndarray:
+    """The reference tests' deterministic LCG, (s / divisor) * 2 - 1 per
+    step: divisor 2^32 gives [-1, 1) as tests/fused-sdpa.test.ts:29-38;
+    randBf16 of tests/fused-decode-kernel.test.ts:16-28 divides by
+    0xffffffff (and halves the result)."""
     out = np.empty(n, dtype=np.float32)
     s = seed & 0xFFFFFFFF
     for i in range(n):
         s = (s * 1664525 + 1013904223) & 0xFFFFFFFF
-        out[i] = np.float32((s / 2 ** 32) * 2 - 1)
+        out[i] = np.float32((s / divisor) * 2 - 1)
     return out
+
+
+def rand_bf16_ref(shape, seed: int) -> np.ndarray:
+    """randBf16 of tests/fused-decode-kernel.test.ts:16-28: the LCG over
+    0xffffffff, times 0.5, rounded to bf16 (as float32)."""
+    n = int(np.prod(shape))
+    return round_t((lcg_floats(n, seed, 0xFFFFFFFF) * np.float32(0.5)).reshape(shape), BF16)

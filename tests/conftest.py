@@ -44,22 +44,44 @@ def half_ulp(ref, dtype):
     return 0.5 * 2.0 ** (np.floor(np.log2(a)) - mant)
 
 
+# worst |err| / tol of every assert_close call, reported at the end of the run
+HEADROOM = []
+
+
 def assert_close(got, ref, atol=1e-2, rtol=1e-3, what="", dtype=None):
     """|got - ref| <= atol + rtol |ref| (+ half an ulp of T when the output is
     rounded to T = `dtype`): the attention / matmul bar against the fp32
     reference -- fp32 accumulation within max-abs 1e-2 and relative 1e-3,
-    then the one rounding every T-typed output carries."""
+    then the one rounding every T-typed output carries.  Returns the worst
+    |err| / tol (1.0 = at the bar) and records it for the run summary."""
     got = np.asarray(got, dtype=np.float64)
     ref = np.asarray(ref, dtype=np.float64)
     assert got.shape == ref.shape, (got.shape, ref.shape)
     assert np.all(np.isfinite(got)), f"{what}: non-finite output"
     err = np.abs(got - ref)
     tol = atol + rtol * np.abs(ref) + half_ulp(ref, dtype)
+    ratio = float((err / tol).max()) if err.size else 0.0
+    test = os.environ.get("PYTEST_CURRENT_TEST", "").split(" ")[0].split("::")[-1]
+    HEADROOM.append((test, what, ratio, float(err.max()) if err.size else 0.0))
     bad = err > tol
     if bad.any():
         i = np.unravel_index(np.argmax(err - tol), err.shape)
         raise AssertionError(f"{what}: {bad.sum()} / {bad.size} elements out of tolerance; worst at {i}: "
-                             f"got {got[i]} ref {ref[i]} (max abs err {err.max():.3g})")
+                             f"got {got[i]} ref {ref[i]} (max abs err {err.max():.3g}, worst err/tol {ratio:.3f})")
+    return ratio
+
+
+def pytest_terminal_summary(terminalreporter):
+    """Per test, the worst err/tol ratio of its assert_close checks."""
+    if not HEADROOM:
+        return
+    worst = {}
+    for test, what, ratio, err in HEADROOM:
+        if test not in worst or ratio > worst[test][1]:
+            worst[test] = (what, ratio, err)
+    terminalreporter.section("parity headroom: worst |err| / tol per test (1.0 = at the bar)")
+    for test, (what, ratio, err) in sorted(worst.items(), key=lambda kv: -kv[1][1]):
+        terminalreporter.write_line(f"{ratio:6.3f}  max|err| {err:.3g}  {test}  [{what}]")
 
 
 def write_safetensors(path, tensors, metadata=None):

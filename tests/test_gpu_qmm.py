@@ -294,3 +294,35 @@ def test_gather_qmm_sorted_bad_index_and_repeat(O, mlxq_dev, experts_small):
     x2 = rng_t(O, (96, 1, 512), 78, BF16)
     got2 = _gather(O, x2, wq, idx2, 64, 4, BF16, sorted_indices=True)
     assert_close(got2, _sorted_ref(x2, wd, idx2), what="sorted second call", dtype=BF16)
+
+
+@pytest.fixture(scope="module")
+def experts_many(O):
+    """512 experts W [128, 256] ~ N(0, 0.02^2), 4-bit group 64, with their
+    float64 dequantization (few rows an expert: 32-row GEMM blocks)."""
+    w = rng_t(O, (512, 128, 256), 43, BF16, 0.02)
+    wq = O.quantize(w, 64, 4, BF16)
+    wd = deq64(O, wq[0], wq[1], wq[2], 64, 4, BF16)
+    return wq, wd
+
+
+@pytest.mark.parametrize("rows,experts", [(16384, "few"), (16384, "many"), (20000, "few"), (20000, "many")])
+def test_gather_qmm_sorted_past_one_index_stage(O, mlxq_dev, experts_small, experts_many, rows, experts):
+    """The segments kernel stages 16384 indices per load phase: 16384 rows
+    (the reference's 2048-token prefill chunk x top-8) end exactly on the
+    stage boundary, 20000 rows cross it with one expert's run straddling row
+    16384 (its carry across phases).  16 experts give 64-row blocks, 512
+    experts 32-row blocks.  Against the fp64 reference and the per-row
+    gather."""
+    wq, wd = experts_small if experts == "few" else experts_many
+    E, K = wd.shape[0], wd.shape[2]
+    r = np.random.default_rng(rows + E)
+    idx = np.sort(r.integers(0, E, rows)).astype(np.uint32)
+    if rows > 16384:
+        idx[16360:16410] = idx[16360]  # one run across the stage boundary (order kept)
+        assert idx[16383] == idx[16384]
+    x = rng_t(O, (rows, 1, K), 90 + rows, BF16)
+    got = _gather(O, x, wq, idx, 64, 4, BF16, sorted_indices=True)
+    assert_close(got, _sorted_ref(x, wd, idx), what=f"sorted gather {rows} rows, {E} experts", dtype=BF16)
+    per_row = _gather(O, x, wq, idx, 64, 4, BF16)
+    assert_close(got, per_row, what="sorted vs per-row", dtype=BF16)

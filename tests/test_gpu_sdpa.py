@@ -80,6 +80,16 @@ def test_decode_batched_ring_window(O, mlxq_dev):
     check(O, got, q, kq, vq, BF16, 1.0, 64, 4, "c3", valid_len=lens, ring_off=ring)
 
 
+@pytest.mark.parametrize("Hq,Hkv,D", [(32, 8, 128), (16, 8, 256)])
+def test_decode_32k_scale_one(O, mlxq_dev, Hq, Hkv, D):
+    """Gemma4 calls quantizedSdpa with scale 1 (src/model/gemma4-base.ts:1282-1285):
+    unit-normal q and k then give scores with a spread of sqrt(D), the most
+    peaked softmax the decode kernels see.  The 32k-context shape (nRep 4,
+    D 128) and the D 256 / nRep 2 shape at 32k, 4-bit group 64, bf16."""
+    q, kq, vq = case(O, 1, Hq, Hkv, 1, 32768, D, 64, 4, BF16, 21 + D)
+    check(O, run(O, mlxq_dev, q, kq, vq, BF16, 1.0, 64, 4), q, kq, vq, BF16, 1.0, 64, 4, f"32k scale 1 D{D}")
+
+
 @pytest.mark.parametrize("B,Hq,Hkv,N,D,gs,bits,dtype", [
     (1, 4, 2, 333, 256, 64, 4, BF16),     # fused-decode-kernel.test.ts site shapes, N=333
     (1, 4, 2, 333, 256, 64, 8, BF16),
@@ -171,12 +181,15 @@ def test_prefill_causal(O, mlxq_dev, L, N, window):
     check(O, got, q, kq, vq, BF16, 0.125, 64, 4, "prefill", causal=True, window=window)
 
 
-def test_reference_lcg_case_tiled_bound(O, mlxq_dev):
-    """tests/fused-sdpa.test.ts 'multi-tile kv4': our prefill vs the reference's
-    tiled restatement within its 2/128 bound."""
+@pytest.mark.parametrize("KV,nRep,L,N,D,gs,bits", [  # tests/fused-sdpa.test.ts:66-72
+    (2, 4, 96, 448, 64, 64, 8), (2, 4, 96, 1217, 64, 64, 8), (2, 4, 96, 1217, 64, 64, 4),
+    (4, 1, 64, 700, 64, 32, 8), (1, 16, 48, 1100, 512, 64, 8)])
+def test_reference_lcg_case_tiled_bound(O, mlxq_dev, KV, nRep, L, N, D, gs, bits):
+    """tests/fused-sdpa.test.ts's five cases (single / multi tile, kv4 and
+    kv8, no GQA, the 12B full-attention shape): our prefill vs the
+    reference's tiled restatement within its 2/128 bound, on its LCG data."""
     from mlxq import ops
 
-    KV, nRep, L, N, D, gs, bits = 2, 4, 96, 1217, 64, 64, 4
     H = KV * nRep
     bf = O.BF16
     q = O.round_t(O.lcg_floats(H * L * D, 17).reshape(1, H, L, D), bf)
@@ -186,17 +199,18 @@ def test_reference_lcg_case_tiled_bound(O, mlxq_dev):
     got = run(O, mlxq_dev, q, kq, vq, bf, 0.125, gs, bits, mask=ops.Mask("causal"))
     tiled = O.sdpa_tiled_t(q, kq, vq, scale=0.125, gs=gs, bits=bits, dtype=bf, causal=True)
     assert np.abs(got - tiled).max() <= 2 / 128
+    check(O, got, q, kq, vq, bf, 0.125, gs, bits, "lcg case", causal=True)
 
 
 @pytest.mark.parametrize("site", [(4, 2, 256, 64, 4), (4, 2, 256, 64, 8), (16, 1, 512, 64, 4)])
 def test_reference_decode_sites_vs_unfused(O, mlxq_dev, site):
-    """tests/fused-decode-kernel.test.ts:30-67: LCG data * 0.5, N = 333, the
+    """tests/fused-decode-kernel.test.ts:30-67: its randBf16 data, N = 333, the
     12B's three dispatch-site shapes; bounded divergence < 0.02 from the
     unfused path and non-trivial outputs."""
     H, KV, D, gs, bits = site
     N = 333
     bf = O.BF16
-    mk = lambda shape, seed: O.round_t(O.lcg_floats(int(np.prod(shape)), seed).reshape(shape) * 0.5, bf)
+    mk = O.rand_bf16_ref
     q, k, v = mk((1, H, 1, D), 11), mk((1, KV, N, D), 22), mk((1, KV, N, D), 33)
     kq, vq = O.quantize(k, gs, bits, bf), O.quantize(v, gs, bits, bf)
     got = run(O, mlxq_dev, q, kq, vq, bf, 1.0, gs, bits)

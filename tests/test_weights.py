@@ -49,6 +49,32 @@ def test_rejects_size_mismatch_and_overrun(tmp_path):
         SafetensorsFile(p)
 
 
+def test_rejects_negative_or_reversed_offsets(tmp_path):
+    """data_offsets must satisfy 0 <= begin <= end (a negative begin would
+    read header bytes as tensor data)."""
+    from mlxq.weights import SafetensorsFile
+
+    p = str(tmp_path / "neg.safetensors")
+    for offs in ([-8, 8], [16, 0]):
+        hb = json.dumps({"t": {"dtype": "F32", "shape": [4], "data_offsets": offs}}).encode()
+        with open(p, "wb") as f:
+            f.write(struct.pack("<Q", len(hb)) + hb + b"\0" * 16)
+        with pytest.raises(ValueError, match="out of order"):
+            SafetensorsFile(p)
+
+
+def test_sharded_index_rejects_paths_outside_the_model_dir(tmp_path):
+    from mlxq.weights import ShardedSafetensors
+
+    model = tmp_path / "model"
+    model.mkdir()
+    write_safetensors(str(tmp_path / "outside.safetensors"), {"t": ("F32", (1,), np.zeros(1, np.float32).tobytes())})
+    with open(model / "model.safetensors.index.json", "w") as f:
+        json.dump({"weight_map": {"t": "../outside.safetensors"}}, f)
+    with pytest.raises(ValueError, match="outside the model directory"):
+        ShardedSafetensors(str(model))
+
+
 def test_sharded_index(tmp_path):
     from mlxq.weights import ShardedSafetensors
 
