@@ -30,7 +30,7 @@ Also measured in the same run and reported beside it:
                         causal chunk over 8192 keys
   cpu_baseline          the CPU oracle's decode on the host, bounded sample
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--quick]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--quick] [--only SECTIONS]
 """
 from __future__ import annotations
 
@@ -406,6 +406,22 @@ def traffic_bytes():
 
 # --------------------------------------------------------------------- main
 
+SECTIONS = ("decode", "qmm", "decode_1k", "ring", "moe", "moe_sorted", "tied_head", "prefill", "gemma4")
+
+
+def copy_calibration(timer, nbytes=256 << 20, steps=20):
+    """A device-to-device copy of a known size (the reference point that
+    scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes)."""
+    from mlxq import _lib
+    from mlxq.array import DeviceArray
+
+    src, dst = DeviceArray.empty((nbytes,), 3), DeviceArray.empty((nbytes,), 3)
+    src_p, dst_p = src.ptr, dst.ptr
+    ms = timer.graph_step_ms(lambda i: _lib.call("mlxq_memcpy_dtod", dst_p, src_p, nbytes // 4 * 4, None), steps, 2)
+    return {"bytes_per_copy": nbytes // 4 * 4, "us_per_copy": round(ms * 1e3, 2),
+            "GB/s (read + write)": round(2 * nbytes / (ms * 1e-3) / 1e9, 1)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -413,12 +429,23 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--quick", action="store_true", help="headline decode and qmv M=1 only")
+    ap.add_argument("--only", default=None,
+                    help="comma list of sections to run (profiling runs): " + ", ".join(SECTIONS) +
+                         ", copy (a 256 MiB device copy: the PMC byte-counter reference)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "runs on one GPU only: decode shards over (batch, kv head) or splits the "
                                    "sequence with one all-gather of fp32 partials, which is not launched here",
                           "n_gpus": args.gpus}))
         sys.exit(2)
+    if args.only:
+        want = set(args.only.split(","))
+        bad = want - set(SECTIONS) - {"copy"}
+        if bad:
+            ap.error(f"unknown sections {sorted(bad)}")
+    else:
+        want = {"decode", "qmm"} if args.quick else set(SECTIONS)
+    run = want.__contains__
 
     import mlxq
     from mlxq import _lib
@@ -426,34 +453,39 @@ def main():
     mlxq.ensure_init(0)
     timer = Timer(_lib.lib())
 
-    log("bench: 32k decode (headline)")
-    launch, algo_bytes, keep = decode_workload()
-    ms_step = timer.graph_step_ms(launch, args.steps, args.warmup)
-    mean_us, med_us = timer.per_launch_us(launch, 100)
-    value = algo_bytes / (ms_step * 1e-3) / 1e9
-    del keep
+    value = ms_step = mean_us = med_us = algo_bytes = None
+    if run("decode"):
+        log("bench: 32k decode (headline)")
+        launch, algo_bytes, keep = decode_workload()
+        ms_step = timer.graph_step_ms(launch, args.steps, args.warmup)
+        mean_us, med_us = timer.per_launch_us(launch, 100)
+        value = algo_bytes / (ms_step * 1e-3) / 1e9
+        del keep
 
     extra = {}
-    log("bench: qmv / qmm")
     qmm = []
-    shapes = [(1, 14336, 4096)] if args.quick else [(m, n, k) for (n, k) in ((14336, 4096), (4096, 14336))
-                                                     for m in (1, 4, 16, 64)]
-    for M, N, K in shapes:
-        ql, qb, qk = qmv_workload(M=M, N=N, K=K)
-        q_ms = timer.graph_step_ms(ql, 100, 10)
-        qmm.append({"M": M, "N": N, "K": K, "us_per_call": round(q_ms * 1e3, 3),
-                    "GB/s": round(qb / (q_ms * 1e-3) / 1e9, 1), "pct_hbm_peak": round(100 * qb / (q_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 1),
-                    "TFLOP/s": round(2 * M * N * K / (q_ms * 1e-3) / 1e12, 2), "algorithmic_bytes": qb})
-        del qk
-    extra["qmv_qmm"] = qmm
+    if run("qmm"):
+        log("bench: qmv / qmm")
+        shapes = [(1, 14336, 4096)] if args.quick else [(m, n, k) for (n, k) in ((14336, 4096), (4096, 14336))
+                                                         for m in (1, 4, 16, 64)]
+        for M, N, K in shapes:
+            ql, qb, qk = qmv_workload(M=M, N=N, K=K)
+            q_ms = timer.graph_step_ms(ql, 100, 10)
+            qmm.append({"M": M, "N": N, "K": K, "us_per_call": round(q_ms * 1e3, 3),
+                        "GB/s": round(qb / (q_ms * 1e-3) / 1e9, 1),
+                        "pct_hbm_peak": round(100 * qb / (q_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 1),
+                        "TFLOP/s": round(2 * M * N * K / (q_ms * 1e-3) / 1e12, 2), "algorithmic_bytes": qb})
+            del qk
+        extra["qmv_qmm"] = qmm
 
-    if not args.quick:
+    if run("decode_1k"):
         log("bench: decode fp16 8-bit 1k")
         l1, b1, k1 = decode_workload(B=1, Hq=16, Hkv=4, D=128, N=1024, gs=64, bits=8, dtype=F16)
         ms1 = timer.graph_step_ms(l1, 200, 20)
         extra["decode_fp16_8bit_1k"] = {"us_per_call": round(ms1 * 1e3, 3), "algorithmic_bytes": b1,
                                         "GB/s": round(b1 / (ms1 * 1e-3) / 1e9, 1)}
         del k1
+    if run("ring"):
         log("bench: batched ring decode")
         l3, b3, k3 = batched_ring_workload()
         ms3 = timer.graph_step_ms(l3, 50, 5)
@@ -461,6 +493,7 @@ def main():
                                         "GB/s": round(b3 / (ms3 * 1e-3) / 1e9, 1),
                                         "pct_hbm_peak": round(100 * b3 / (ms3 * 1e-3) / 1e9 / HBM_PEAK_GBS, 1)}
         del k3
+    if run("moe"):
         log("bench: MoE gather_qmm decode")
         moe = {}
         for name, (n, k) in (("gate_up", (1408, 2816)), ("down", (2816, 704))):
@@ -471,6 +504,7 @@ def main():
                          "pct_hbm_peak": round(100 * bm / (msm * 1e-3) / 1e9 / HBM_PEAK_GBS, 1)}
             del km
         extra["moe_gather_decode"] = moe
+    if run("moe_sorted"):
         log("bench: MoE gather_qmm, sorted prefill rows")
         ls_, lr_, bs_, fs_, ks_ = moe_sorted_workload(1408, 2816)
         mss = timer.graph_step_ms(ls_, 20, 3)
@@ -481,6 +515,7 @@ def main():
             "algorithmic_bytes": bs_, "GB/s": round(bs_ / (mss * 1e-3) / 1e9, 1),
             "TFLOP/s": round(fs_ / (mss * 1e-3) / 1e12, 1)}
         del ks_
+    if run("tied_head"):
         log("bench: tied head")
         lh, bh, kh = tied_head_workload()
         msh = timer.graph_step_ms(lh, 50, 5)
@@ -489,6 +524,7 @@ def main():
                                   "GB/s": round(bh / (msh * 1e-3) / 1e9, 1),
                                   "pct_hbm_peak": round(100 * bh / (msh * 1e-3) / 1e9 / HBM_PEAK_GBS, 1)}
         del kh
+    if run("prefill"):
         log("bench: chunked prefill")
         l5, f5, k5 = prefill_workload()
         m5, md5 = timer.per_launch_us(l5, 10)
@@ -496,6 +532,7 @@ def main():
                                   "TFLOP/s": round(f5 / (md5 * 1e-6) / 1e12, 1),
                                   "pct_mfma_bf16_peak": round(100 * f5 / (md5 * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 1)}
         del k5
+    if run("gemma4"):
         log("bench: gemma4 full attention (D 512)")
         g4 = {}
         lg, bg, kg = decode_workload(B=1, Hq=16, Hkv=2, D=512, N=32768, gs=64, bits=4)
@@ -511,13 +548,22 @@ def main():
                                   "pct_mfma_bf16_peak": round(100 * fp / (mdp * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 1)}
         del kpw
         extra["gemma4_full_attention"] = g4
+    if run("copy"):
+        log("bench: device copy (counter reference)")
+        extra["device_copy"] = copy_calibration(timer)
 
     cpu = None
-    if not args.no_cpu:
+    if not args.no_cpu and run("decode"):
         log("bench: cpu baseline")
         cpu = cpu_baseline()
 
-    qmv1 = qmm[0]
+    if value is None:
+        # a profiling run without the headline section: report what ran
+        print(json.dumps({"metric": METRIC, "value": None, "sections": sorted(want), "other_configs": extra}),
+              flush=True)
+        return
+    qmv1 = qmm[0] if qmm else None
+    traffic = traffic_bytes()
     line = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -545,14 +591,20 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(value / HBM_PEAK_GBS, 4),
-            "traffic": traffic_bytes(),
+            "traffic": traffic,
+            "traffic_source": ("not measured in this run: HBM bytes per decode call (partial + merge kernel) from "
+                               "the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes over this workload, scaled "
+                               "by a 256 MiB device copy of the same run (profiles/decode_32k_traffic.json, "
+                               "profiles/bench_kernels_pmc_counters.txt)")
+            if traffic is not None else None,
             "kernel": "decode call = sdpa_decode_mfma_kernel + sdpa_decode_merge_kernel (graph-replayed, "
                       "per-step time)",
             "single_call_us_mean": round(mean_us, 3),
             "single_call_us_median": round(med_us, 3),
         },
-        "qmv": {"workload": "x [1, 4096] bf16 @ W [14336, 4096]^T, 4-bit group 64",
-                "GB/s": qmv1["GB/s"], "us_per_call": qmv1["us_per_call"], "pct_hbm_peak": qmv1["pct_hbm_peak"]},
+        "qmv": ({"workload": "x [1, 4096] bf16 @ W [14336, 4096]^T, 4-bit group 64",
+                 "GB/s": qmv1["GB/s"], "us_per_call": qmv1["us_per_call"], "pct_hbm_peak": qmv1["pct_hbm_peak"]}
+                if qmv1 else None),
         "other_configs": extra,
         "cpu_baseline": cpu,
     }
