@@ -230,6 +230,28 @@ int mlxq_quantized_sdpa(const void* q, int dtype, int B, int Hq, int Hkv, int Lq
                         const int32_t* ring_offset, int mask_mode, int window, float scale,
                         int group_size, int bits, void* out, void* stream);
 
+/* mlxq_quantized_sdpa without any device allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory -- code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc.  Same arguments, kernels and results as mlxq_quantized_sdpa;
+ * its scratch (the split-K partials of decode and of the split wide
+ * prefill) is a fixed block of MLXQ_NOALLOC_SCRATCH_BYTES per device, held
+ * from mlxq_init until the process ends, instead of the growable workspace.
+ * A request whose partials need more fails with MLXQ_ERR_UNSUPPORTED before
+ * any launch (a 32k-context decode needs about 0.5 MB; the 32-row, 4096-slot
+ * D 256 ring decode 2.7 MB; a split D 512 prefill chunk of 512 queries
+ * 33 MB).  Every call on a device shares that device's block and nothing in
+ * it needs to start at zero (partials are written before they are read);
+ * calls that overlap on one device (two streams, or this call beside a
+ * replay of a graph that captured it) race on it. */
+#define MLXQ_NOALLOC_SCRATCH_BYTES (8u << 20)
+int mlxq_quantized_sdpa_noalloc(const void* q, int dtype, int B, int Hq, int Hkv, int Lq, int D,
+                                const uint32_t* k_packed, const void* k_scales, const void* k_biases,
+                                const uint32_t* v_packed, const void* v_scales, const void* v_biases,
+                                int64_t kv_capacity, int64_t n_kv, const int32_t* valid_len,
+                                const int32_t* ring_offset, int mask_mode, int window, float scale,
+                                int group_size, int bits, void* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

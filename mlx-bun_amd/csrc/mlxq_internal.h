@@ -60,6 +60,10 @@ struct Scratch {
   int get(size_t bytes, void** out, hipStream_t stream) const;
 };
 
+// The no-allocation entry points' fixed block on the current device: its
+// device address (looked up once per device at mlxq_init) and size.
+int noalloc_scratch(Scratch* out);
+
 inline bool is_half_dtype(int dtype) { return dtype == MLXQ_FLOAT16 || dtype == MLXQ_BFLOAT16; }
 inline bool dtype_supported(int dtype) { return is_half_dtype(dtype) || dtype == MLXQ_FLOAT32; }
 inline int dtype_bytes(int dtype) { return dtype == MLXQ_FLOAT32 ? 4 : 2; }

@@ -28,6 +28,14 @@ struct DeviceWorkspace {
 static std::vector<DeviceWorkspace> g_ws;  // indexed by device
 static int g_live_graphs = 0;              // graph execs made by mlxq_graph_end, not yet destroyed
 
+// The fixed scratch block of the no-allocation entry points: a file-scope
+// device array, so every GPU the library runs on holds its own copy for the
+// life of the process.  In host code `scratch` names a host-side stand-in,
+// not device memory: its per-device address comes from hipGetSymbolAddress
+// at mlxq_init (g_scratch_ptr), and only that address reaches kernels.
+static __device__ __align__(256) uint8_t scratch[MLXQ_NOALLOC_SCRATCH_BYTES];
+static std::vector<void*> g_scratch_ptr;  // indexed by device
+
 void set_error(const std::string& msg) { g_last_error = msg; }
 
 int fail(int code, const std::string& msg) {
@@ -86,6 +94,17 @@ int workspace(size_t bytes, void** out, hipStream_t stream) {
   return MLXQ_OK;
 }
 
+int noalloc_scratch(Scratch* out) {
+  int dev = 0;
+  MLXQ_HIP(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (dev >= (int)g_scratch_ptr.size() || !g_scratch_ptr[dev])
+    return fail(MLXQ_ERR_STATE, "mlxq_init was not called for the current device");
+  out->fixed = g_scratch_ptr[dev];
+  out->fixed_bytes = MLXQ_NOALLOC_SCRATCH_BYTES;
+  return MLXQ_OK;
+}
+
 int Scratch::get(size_t bytes, void** out, hipStream_t stream) const {
   if (!fixed) return workspace(bytes, out, stream);
   if (bytes > fixed_bytes)
@@ -131,6 +150,12 @@ int mlxq_init(int device) {
     return fail(MLXQ_ERR_UNSUPPORTED, "libmlxq is built for gfx950 only; device is " + arch);
   std::lock_guard<std::mutex> lk(g_mu);
   if (!g_stream) MLXQ_HIP(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
+  if ((int)g_scratch_ptr.size() <= device) g_scratch_ptr.resize(device + 1, nullptr);
+  if (!g_scratch_ptr[device]) {  // this device's copy of the fixed scratch block
+    void* p = nullptr;
+    MLXQ_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    g_scratch_ptr[device] = p;
+  }
   g_cu_count = prop.multiProcessorCount;
   g_device = device;
   return MLXQ_OK;

@@ -2267,3 +2267,18 @@ extern "C" int mlxq_quantized_sdpa(const void* q, int dtype, int B, int Hq, int 
                        kv_capacity, n_kv, valid_len, ring_offset, mask_mode, window, scale, group_size, bits, out,
                        stream, mlxq::Scratch{});
 }
+
+extern "C" int mlxq_quantized_sdpa_noalloc(const void* q, int dtype, int B, int Hq, int Hkv, int Lq, int D,
+                                           const uint32_t* k_packed, const void* k_scales, const void* k_biases,
+                                           const uint32_t* v_packed, const void* v_scales, const void* v_biases,
+                                           int64_t kv_capacity, int64_t n_kv, const int32_t* valid_len,
+                                           const int32_t* ring_offset, int mask_mode, int window, float scale,
+                                           int group_size, int bits, void* out, void* stream) {
+  MLXQ_REQUIRE_INIT();
+  mlxq::Scratch scr;
+  const int rc = mlxq::noalloc_scratch(&scr);
+  if (rc) return rc;
+  return sdpa_dispatch(q, dtype, B, Hq, Hkv, Lq, D, k_packed, k_scales, k_biases, v_packed, v_scales, v_biases,
+                       kv_capacity, n_kv, valid_len, ring_offset, mask_mode, window, scale, group_size, bits, out,
+                       stream, scr);
+}
