@@ -132,6 +132,19 @@ __device__ __forceinline__ uint32_t perm_b32(uint32_t hi, uint32_t lo, uint32_t 
   return __builtin_amdgcn_perm(hi, lo, sel);
 }
 
+// 4 x 4 dword transpose across the lane quarters (lanes l, l+16, l+32, l+48):
+// on entry quarter q holds a_q[0..3]; on exit word k of quarter q is a_k[q].
+__device__ __forceinline__ void quarter_transpose(uint32_t (&w)[4]) {
+  auto s02 = __builtin_amdgcn_permlane32_swap(w[0], w[2], false, false);
+  auto s13 = __builtin_amdgcn_permlane32_swap(w[1], w[3], false, false);
+  auto s01 = __builtin_amdgcn_permlane16_swap(s02[0], s13[0], false, false);
+  auto s23 = __builtin_amdgcn_permlane16_swap(s02[1], s13[1], false, false);
+  w[0] = s01[0];
+  w[1] = s01[1];
+  w[2] = s23[0];
+  w[3] = s23[1];
+}
+
 // ---- code -> operand conversion --------------------------------------------
 //
 // The 8 k slots of one operand come from 8 consecutive codes of a row.  The

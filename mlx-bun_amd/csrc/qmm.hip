@@ -303,6 +303,349 @@ __global__ void __launch_bounds__(512) qmv_kernel(const uint16_t* __restrict__ x
   }
 }
 
+// ---- streaming MFMA GEMM for 8 < M <= 64 (4-bit, transpose = true) -------
+//
+// A workgroup owns R = 4 weight row tiles (64 rows) and a range of 128-code
+// K tiles, for all M activation rows (MB = ceil(M / 16) MFMA row blocks), so
+// each weight operand serves all of M and each x operand every row tile of
+// its consumer.  Its 12 waves split the work:
+//   * waves 8..11 (producers) stage x through LDS in chunks of 4 K tiles
+//     (double buffered, pre-permuted into the code slot order); their loads
+//     come from L2 (every workgroup reads all of x);
+//   * waves 0..7 (consumers, two per SIMD so one's MFMAs cover the other's
+//     LDS reads and fold) take K tile w % 4 of each chunk for row tiles
+//     2 (w / 4) and 2 (w / 4) + 1: its weights (one dwordx4 per lane per row
+//     tile, 16 rows x 64 contiguous bytes, then a 4 x 4 dword transpose across
+//     the lane quarters so k-step j holds codes 32 j .. 32 j + 31 and never
+//     leaves a quantization group), scales and biases stream PF chunks ahead
+//     through registers; per group X = x against ones (row sums) and D = x
+//     against the exact code operands fold as acc += s D + (b - OFF s) X.
+// Only the consumers' queues hold the weight stream and only the producers'
+// the x loads, so neither waits for the other's loads (vector loads complete
+// in order); one LDS-only barrier per chunk hands the buffers over.  The
+// consumers' accumulators are summed in LDS in fixed order; workgroups of a
+// K split (blockIdx.z = batch * KS + split) write fp32 partials for
+// qmm_splitk_reduce_kernel.  Rows past M or N read zeros and are not stored.
+template <int MB, int NC_>
+struct StreamShape {
+  static constexpr int R = 4;            // weight row tiles per workgroup
+  static constexpr int C = 4;            // K tiles per chunk
+  static constexpr int NC = NC_;         // consumer waves: K tile (w % C), row tiles RC (w / C) ..
+  static constexpr int RC = R * C / NC;  // row tiles per consumer
+  static constexpr int NP = 4;           // producer waves
+  static constexpr int NT = 64 * (NC + NP);
+  static constexpr int CK = C * 128;     // codes (x values) per chunk row
+  static constexpr int BLOCKS = MB * C * 4;                 // 1 KB operand blocks per chunk
+  static constexpr int XBUF = BLOCKS * 1024;                // bytes per x buffer
+  static constexpr int RED = NC * RC * MB * 64 * 16;        // consumer reduction
+  static constexpr int LDS = 2 * XBUF > RED ? 2 * XBUF : RED;
+  static constexpr int BPW = BLOCKS / NP;                   // blocks per producer wave
+  static_assert(BLOCKS % NP == 0 && RC >= 1, "work split");
+};
+
+template <typename T, int GS, int MB, int NC_, int PF>
+__global__ void __launch_bounds__(64 * (NC_ + 4)) qmm_stream_kernel(const uint16_t* __restrict__ x, int M, int K,
+                                                         const uint32_t* __restrict__ w,
+                                                         const uint16_t* __restrict__ scales,
+                                                         const uint16_t* __restrict__ biases, int N, BatchMap bm,
+                                                         int KS, int KTS, uint16_t* __restrict__ y,
+                                                         float* __restrict__ part) {
+  using SH = StreamShape<MB, NC_>;
+  static_assert(SH::NT == 64 * (NC_ + 4), "launch bounds");
+  using CO = CodeOps<T, 4>;
+  constexpr int R = SH::R, C = SH::C, BPW = SH::BPW, NC = SH::NC, RC = SH::RC;
+  constexpr int NG = 128 / GS;  // quantization groups per K tile (1 or 2)
+  constexpr int KPG = GS / 32;  // k-steps per group
+  constexpr float OFF = CO::OFFSET;
+  static_assert(GS == 64 || GS == 128, "group size");
+  // x chunks in LDS in MFMA operand order: block (b, kt, j) of buffer p is
+  // the A operand of row block b, K tile kt of the chunk, k-step j (1 KB,
+  // 16 bytes a lane, lane l = row l % 16, x values 8 (l / 16) .. + 8)
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ln = lane & 15, lq = lane >> 4;
+  const int bidx = blockIdx.z / KS, split = blockIdx.z % KS;
+  int64_t xb, wb;
+  bool xok, wok;
+  bm.resolve(bidx, xb, xok, wb, wok);
+  const int n0 = blockIdx.x * 16 * R;
+  const int nrows = wok ? min(16 * R, N - n0) : 0;
+  const int G = K / GS, KT = K / 128;
+  const int sk0 = split * KTS, sk1 = min(KT, sk0 + KTS);
+  const int nch = (sk1 - sk0 + C - 1) / C;  // chunks of this workgroup
+  // the consumers' chunk loop runs a multiple of PF chunks with no branch
+  // around its loads (so the waits before a chunk leave the later chunks'
+  // loads in flight); chunks past nch compute with zero scales (adding 0)
+  const int ncp = (nch + PF - 1) / PF * PF;
+  const uint32_t row_bytes = (uint32_t)K / 2;
+  // workgroups start at different chunks (in order of their launch on one
+  // XCD, blockIdx.x / 8), so the XCD's workgroups do not all read the same x
+  // lines at once; chunk c of the loop is chunk phys(c) of the split
+  const int spread = nch > 0 ? 1 << (31 - __builtin_clz(nch)) : 1;  // largest power of 2 <= nch
+  const int rot = (int)((blockIdx.x >> 3) + blockIdx.z) & (spread - 1);
+  // (past nch: any chunk; those loads are clamped and their terms zeroed)
+  auto phys = [&](int c) {
+    const int q = c + rot;
+    return q >= nch ? q - nch : q;
+  };
+
+  if (wave >= NC) {
+    // ---------------------------------------------------------- producers
+    // producer wave pw stages k-step pw of every (row block, K tile) of each
+    // chunk: lane l loads x row 16 b + l % 16, values 8 (l / 16) .. + 8 of
+    // the k-step (64 bytes of each of 16 rows per load, from L2)
+    static_assert(SH::NP == 4 && BPW == MB * C, "one k-step per producer wave");
+    const int pw = wave - NC;
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + xb * M * K, xok ? (uint32_t)M * (uint32_t)K * 2u : 0u);
+    uint32_t vrow[MB];  // row part of each row block's offsets (rows past M: past the descriptor)
+#pragma unroll
+    for (int b = 0; b < MB; b++)
+      vrow[b] = 16 * b + ln < M ? (uint32_t)(16 * b + ln) * (uint32_t)K * 2u + 16u * lq : 0x80000000u;
+    // two register buffers: chunk c is staged from one, which then takes
+    // chunk c + 2's loads, so two chunks stay in flight across the barriers
+    // (a chunk past nch reads zeros: every offset is pushed past the
+    // descriptor; staging them is harmless, the consumers give those chunks
+    // zero scales).  Where the registers do not fit beside the consumers'
+    // (8 consumers at MB = 4) one buffer is loaded and staged per chunk.
+    constexpr bool XDB = NC == 4 || MB <= 3;
+    u32x4_t xr[XDB ? 2 : 1][BPW];
+    auto load = [&](u32x4_t (&v)[BPW], int c) {
+#pragma unroll
+      for (int i = 0; i < BPW; i++) {
+        const int kt = sk0 + phys(c) * C + i % C;  // workgroup-uniform
+        const bool ok = (c < nch) & (kt < sk1);
+        const uint32_t col = (uint32_t)(kt * 128 + pw * 32) * 2u;
+        v[i] = buf_load128(rx, ok ? vrow[i / C] + col : 0x80000000u, 0u);
+      }
+    };
+    auto stage = [&](const u32x4_t (&v)[BPW], int c) {
+      uint8_t* dst = smem + (c & 1) * SH::XBUF + (pw * 64 + lane) * 16;
+#pragma unroll
+      for (int i = 0; i < BPW; i++)  // block (i / C, i % C, pw)
+        *reinterpret_cast<u32x4_t*>(dst + i * 4096) = permute8<CO::ORDER>(v[i]);
+    };
+    if constexpr (XDB) {
+      static_assert(PF % 2 == 0, "ncp is a multiple of PF: the pair loop needs it even");
+      // no branch in the loop body (a split body lets the allocator rotate
+      // the buffers, and the copies back would wait for the newest loads)
+      load(xr[0], 0);
+      __builtin_amdgcn_sched_barrier(0);
+      load(xr[1], 1);
+      __builtin_amdgcn_sched_barrier(0);
+      for (int c = 0; c < ncp; c += 2) {
+        stage(xr[0], c);
+        __builtin_amdgcn_sched_barrier(0);
+        load(xr[0], c + 2);
+        __builtin_amdgcn_sched_barrier(0);
+        lds_barrier();  // B_c: chunk c staged / consumers done with chunk c - 1
+        stage(xr[1], c + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        load(xr[1], c + 3);
+        __builtin_amdgcn_sched_barrier(0);
+        lds_barrier();  // B_{c+1}
+      }
+      lds_barrier();  // B_ncp
+    } else {
+      for (int c = 0; c <= ncp; c++) {
+        if (c < nch) {  // workgroup-uniform
+          load(xr[0], c);
+          stage(xr[0], c);
+        }
+        lds_barrier();  // B_c
+      }
+    }
+  } else {
+    // ---------------------------------------------------------- consumers
+    const int kslot = wave % C, rgrp = wave / C;  // K tile of each chunk, row tiles RC rgrp ..
+    const __amdgpu_buffer_rsrc_t rw =
+        make_rsrc(w + ((int64_t)wb * N + n0) * (row_bytes / 4), (uint32_t)nrows * row_bytes);
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(scales + ((int64_t)wb * N + n0) * G, (uint32_t)nrows * (uint32_t)G * 2u);
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(biases + ((int64_t)wb * N + n0) * G, (uint32_t)nrows * (uint32_t)G * 2u);
+    uint32_t wlane[RC], slane[RC];
+#pragma unroll
+    for (int r = 0; r < RC; r++) {
+      const int row = ln + 16 * (RC * rgrp + r);
+      wlane[r] = (uint32_t)row * row_bytes + 16u * lq;
+      slane[r] = (uint32_t)row * (uint32_t)G * 2u;
+    }
+    u32x4_t wr[PF][RC];
+    uint32_t sr[PF][RC], br[PF][RC];
+    // this consumer's K tile of chunk c (past the split's end: the last one
+    // re-read, its contribution zeroed below)
+    auto issue = [&](int slot, int c) {
+      const int kt = min(sk0 + phys(c) * C + kslot, sk1 - 1);
+      const uint32_t woff = (uint32_t)kt * 64u;
+      // GS 64: the dword of groups 2 kt, 2 kt + 1 (4-byte aligned, G even);
+      // GS 128: the one 16-bit group kt (a dword there could cross the end
+      // of the descriptor when G is odd, and would then read as zero)
+      const uint32_t soff = (uint32_t)(kt * NG) * 2u;
+#pragma unroll
+      for (int r = 0; r < RC; r++) wr[slot][r] = buf_load128(rw, wlane[r], woff);
+#pragma unroll
+      for (int r = 0; r < RC; r++) {
+        sr[slot][r] = NG == 2 ? buf_load32(rs, slane[r], soff) : buf_load16(rs, slane[r], soff);
+        br[slot][r] = NG == 2 ? buf_load32(rb, slane[r], soff) : buf_load16(rb, slane[r], soff);
+      }
+    };
+    f32x4_t acc[RC][MB];
+#pragma unroll
+    for (int r = 0; r < RC; r++)
+#pragma unroll
+      for (int b = 0; b < MB; b++) acc[r][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    const u32x4_t ones = {Mma<T>::ONES, Mma<T>::ONES, Mma<T>::ONES, Mma<T>::ONES};
+    const uint32_t magic = opaque(Mma<T>::MAGIC);
+    // slot order is issue order (the scheduler may not interleave slots: a
+    // load of slot 0 issued after slot 1's would make every wait for slot 0
+    // wait for slot 1 too)
+#pragma unroll
+    for (int p = 0; p < PF; p++) {
+      issue(p, p);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    lds_barrier();  // B_0
+    for (int cb = 0; cb < ncp; cb += PF) {
+#pragma unroll
+      for (int p = 0; p < PF; p++) {
+        const int c = cb + p;
+        const bool live = (c < nch) & (sk0 + phys(c) * C + kslot < sk1);  // no branch in the loop body
+        uint32_t wt[RC][4];
+#pragma unroll
+        for (int r = 0; r < RC; r++) {
+          wt[r][0] = wr[p][r].x;
+          wt[r][1] = wr[p][r].y;
+          wt[r][2] = wr[p][r].z;
+          wt[r][3] = wr[p][r].w;
+          quarter_transpose(wt[r]);
+        }
+        float s_g[RC][NG], b_g[RC][NG];
+#pragma unroll
+        for (int r = 0; r < RC; r++) {
+#pragma unroll
+          for (int gi = 0; gi < NG; gi++) {
+            // GS 64: groups 2 kt (low half), 2 kt + 1 (high); GS 128: group kt
+            const int sh = 16 * gi;
+            const float sc = Conv<T>::from_bits((sr[p][r] >> sh) & 0xffffu);
+            const float bi = Conv<T>::from_bits((br[p][r] >> sh) & 0xffffu);
+            s_g[r][gi] = live ? sc : 0.f;
+            b_g[r][gi] = live ? bi - OFF * sc : 0.f;
+          }
+        }
+        const uint8_t* xc = smem + (c & 1) * SH::XBUF + kslot * 4096 + lane * 16;
+        // per group: X[b] = x against ones, D = x against the codes; the
+        // loop order keeps the fewer registers live (all k-steps' x operands
+        // with one row tile's D, or one k-step's with every row tile's D)
+        constexpr bool BY_STEP = RC <= KPG;
+#pragma unroll
+        for (int gi = 0; gi < NG; gi++) {
+          f32x4_t X[MB];
+#pragma unroll
+          for (int b = 0; b < MB; b++) X[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+          auto fold = [&](int r, const f32x4_t (&Dr)[MB]) {
+#pragma unroll
+            for (int b = 0; b < MB; b++)
+#pragma unroll
+              for (int i = 0; i < 4; i++)
+                acc[r][b][i] =
+                    __builtin_fmaf(s_g[r][gi], Dr[b][i], __builtin_fmaf(b_g[r][gi], X[b][i], acc[r][b][i]));
+          };
+          auto xop = [&](int b, int j) {
+            return *reinterpret_cast<const u32x4_t*>(xc + (b * C * 4 + gi * KPG + j) * 1024);
+          };
+          if constexpr (BY_STEP) {
+            f32x4_t D[RC][MB];
+#pragma unroll
+            for (int r = 0; r < RC; r++)
+#pragma unroll
+              for (int b = 0; b < MB; b++) D[r][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < KPG; j++) {
+              u32x4_t a[MB];
+#pragma unroll
+              for (int b = 0; b < MB; b++) {
+                a[b] = xop(b, j);
+                X[b] = Mma<T>::mma(a[b], ones, X[b]);
+              }
+#pragma unroll
+              for (int r = 0; r < RC; r++) {
+                const u32x4_t bop = CO::operand(wt[r][gi * KPG + j], magic);
+#pragma unroll
+                for (int b = 0; b < MB; b++) D[r][b] = Mma<T>::mma(a[b], bop, D[r][b]);
+              }
+            }
+#pragma unroll
+            for (int r = 0; r < RC; r++) fold(r, D[r]);
+          } else {
+            u32x4_t a[MB][KPG];
+#pragma unroll
+            for (int b = 0; b < MB; b++)
+#pragma unroll
+              for (int j = 0; j < KPG; j++) {
+                a[b][j] = xop(b, j);
+                X[b] = Mma<T>::mma(a[b][j], ones, X[b]);
+              }
+#pragma unroll
+            for (int r = 0; r < RC; r++) {
+              f32x4_t D[MB];
+#pragma unroll
+              for (int b = 0; b < MB; b++) D[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+              for (int j = 0; j < KPG; j++) {
+                const u32x4_t bop = CO::operand(wt[r][gi * KPG + j], magic);
+#pragma unroll
+                for (int b = 0; b < MB; b++) D[b] = Mma<T>::mma(a[b][j], bop, D[b]);
+              }
+              fold(r, D);
+            }
+          }
+        }
+        // chunk c + PF's loads go into this slot once its weights are dead
+        // (issued earlier, their registers would overlap the transposed
+        // weights still in use, the allocator would rotate the slots and
+        // the copies back at the loop end would wait for the new loads)
+        __builtin_amdgcn_sched_barrier(0);
+        issue(p, c + PF);
+        __builtin_amdgcn_sched_barrier(0);
+        lds_barrier();  // B_{c+1}
+      }
+    }
+    // the x buffers are free after the last barrier: sum the consumers there
+    f32x4_t* red = reinterpret_cast<f32x4_t*>(smem);  // [NC][RC * MB][64]
+#pragma unroll
+    for (int r = 0; r < RC; r++)
+#pragma unroll
+      for (int b = 0; b < MB; b++) red[(wave * RC * MB + r * MB + b) * 64 + lane] = acc[r][b];
+  }
+  lds_barrier();  // every consumer's accumulators are in LDS
+  if (wave >= NC) return;
+  // output block (row tile rt, row block b) is the sum over the C consumers
+  // of row group rt / RC, in K order; NC waves take the R * MB blocks
+  const f32x4_t* red = reinterpret_cast<const f32x4_t*>(smem);
+  for (int ob = wave; ob < R * MB; ob += NC) {
+    const int rt = ob / MB, b = ob % MB, g = rt / RC, r = rt % RC;
+    f32x4_t v = red[((g * C) * RC * MB + r * MB + b) * 64 + lane];
+#pragma unroll
+    for (int k = 1; k < C; k++) {
+      const f32x4_t o = red[((g * C + k) * RC * MB + r * MB + b) * 64 + lane];
+      v[0] += o[0];
+      v[1] += o[1];
+      v[2] += o[2];
+      v[3] += o[3];
+    }
+    const int n = n0 + 16 * rt + ln;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int m = 16 * b + 4 * lq + i;
+      if (m < M && n < N) {
+        if (KS == 1)
+          y[((int64_t)bidx * M + m) * N + n] = (uint16_t)Conv<T>::to_bits(v[i]);
+        else
+          part[(((int64_t)split * (gridDim.z / KS) + bidx) * M + m) * N + n] = v[i];
+      }
+    }
+  }
+}
+
 // ---- tiled MFMA GEMM over exact code operands (transpose = true) ---------
 //
 // The larger-M path (MLX's qmm stages weight tiles in threadgroup memory as
@@ -756,6 +1099,75 @@ int launch_qmm_tile(const void* x, int64_t batch, int64_t M, int64_t K, const ui
   return launch_qmm_tile_inst<T, BITS, GS, 64, 64>(x, batch, M, K, w, scales, biases, bm, N, y, s);
 }
 
+// MLXQ_QMM_STREAM (A/B tuning): unset or 0 keeps the tiled GEMM for
+// 16 < M <= 64 (the streaming kernel does not beat it yet), 2 routes those
+// shapes to the streaming kernel, 1 also M <= 16 instead of qmv
+// (read on every call, so one process can compare the paths)
+int qmm_stream_override() {
+  const char* e = getenv("MLXQ_QMM_STREAM");
+  return e ? atoi(e) : 0;
+}
+
+template <typename T, int GS, int MB, int NC>
+int launch_qmm_stream_inst(const void* x, int64_t batch, int64_t M, int64_t K, const uint32_t* w,
+                           const void* scales, const void* biases, const BatchMap& bm, int64_t N, void* y,
+                           hipStream_t s) {
+  using SH = StreamShape<MB, NC>;
+  constexpr int PF = 2;
+  const int64_t KT = K / 128;
+  const int64_t groups = (N + 16 * SH::R - 1) / (16 * SH::R);
+  const int64_t cus = mlxq::device_cu_count();
+  // One workgroup fills a CU (its LDS); split K only when the row groups
+  // leave a quarter of the CUs idle, until every CU has one, keeping at
+  // least two chunks per split (each split adds fp32 partial traffic).
+  int KS = 1;
+  const bool can_split = N % 4 == 0 && (uintptr_t)y % 8 == 0;
+  if (can_split && 4 * groups * batch < 3 * cus)
+    while (KS < 16 && groups * batch * KS < cus && KT / (KS * 2) >= 2 * SH::C) KS *= 2;
+  const int ov = qmm_ks_override();
+  if (ov >= 1 && ov <= 16 && (ov == 1 || can_split)) KS = ov;
+  MLXQ_CHECK(batch * KS < 65536, "qmm: batch too large for one launch");
+  const size_t pbytes = KS > 1 ? (size_t)KS * batch * M * N * sizeof(float) : 0;
+  float* part = nullptr;
+  if (pbytes) {
+    void* p = nullptr;
+    int rc = mlxq::workspace(pbytes, &p, s);
+    if (rc) return rc;
+    part = (float*)p;
+  }
+  const int KTS = (int)((KT + KS - 1) / KS);
+  auto kern = qmm_stream_kernel<T, GS, MB, NC, PF>;
+  if (SH::LDS > 64 * 1024) {
+    static bool raised = false;  // per instantiation
+    if (!raised) {
+      MLXQ_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, SH::LDS));
+      raised = true;
+    }
+  }
+  dim3 grid((unsigned)groups, 1, (unsigned)(batch * KS));
+  hipLaunchKernelGGL(kern, grid, dim3(SH::NT), SH::LDS, s, (const uint16_t*)x, (int)M, (int)K, w,
+                     (const uint16_t*)scales, (const uint16_t*)biases, (int)N, bm, KS, KTS, (uint16_t*)y, part);
+  MLXQ_LAUNCHED("qmm_stream_kernel");
+  if (KS > 1) {
+    const int64_t n4 = batch * M * N / 4;
+    hipLaunchKernelGGL((qmm_splitk_reduce_kernel<T>), dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s,
+                       (const float4*)part, n4, KS, (uint2*)y);
+    MLXQ_LAUNCHED("qmm_splitk_reduce_kernel");
+  }
+  return MLXQ_OK;
+}
+
+template <typename T, int GS>
+int launch_qmm_stream(const void* x, int64_t batch, int64_t M, int64_t K, const uint32_t* w, const void* scales,
+                      const void* biases, const BatchMap& bm, int64_t N, void* y, hipStream_t s) {
+  switch ((M + 15) / 16) {
+    case 1: return launch_qmm_stream_inst<T, GS, 1, 8>(x, batch, M, K, w, scales, biases, bm, N, y, s);
+    case 2: return launch_qmm_stream_inst<T, GS, 2, 8>(x, batch, M, K, w, scales, biases, bm, N, y, s);
+    case 3: return launch_qmm_stream_inst<T, GS, 3, 8>(x, batch, M, K, w, scales, biases, bm, N, y, s);
+    default: return launch_qmm_stream_inst<T, GS, 4, 8>(x, batch, M, K, w, scales, biases, bm, N, y, s);
+  }
+}
+
 // ---- generic VALU path -----------------------------------------------------
 // One thread per output element; fp32 accumulation of fp32-dequantized
 // weights.  transpose=1: W [N, K] grouped along K.  transpose=0: W [K, N]
@@ -935,7 +1347,8 @@ int qmm_dispatch(const void* x, int dtype, int64_t batch, int64_t M, int64_t K, 
                       (uintptr_t)w % 16 == 0 && (uintptr_t)scales % 8 == 0 && (uintptr_t)biases % 8 == 0 &&
                       K * M < ((int64_t)1 << 30) && batch < 65536 &&
                       plan_qmv(bits, group_size, M, K, N, batch, &plan);
-  if (qmv_ok) {
+  const int sov = qmm_stream_override();
+  if (qmv_ok && !(sov == 1 && bits == 4)) {
     if (dtype == MLXQ_BFLOAT16) {
       if (bits == 4)
         return group_size == 64 ? launch_qmv<BF16, 4, 64>(x, batch, M, K, w, scales, biases, bm, N, y, plan, s)
@@ -948,6 +1361,21 @@ int qmm_dispatch(const void* x, int dtype, int64_t batch, int64_t M, int64_t K, 
                               : launch_qmv<F16, 4, 128>(x, batch, M, K, w, scales, biases, bm, N, y, plan, s);
     return group_size == 64 ? launch_qmv<F16, 8, 64>(x, batch, M, K, w, scales, biases, bm, N, y, plan, s)
                             : launch_qmv<F16, 8, 128>(x, batch, M, K, w, scales, biases, bm, N, y, plan, s);
+  }
+
+  // 4-bit, 16 < M <= 64 (and M <= 16 when forced): the streaming MFMA GEMM
+  const bool stream_ok = sov >= 1 && (!qmv_ok || sov == 1) && transpose && mlxq::is_half_dtype(dtype) &&
+                         bits == 4 && (group_size == 64 || group_size == 128) && K % 128 == 0 && M >= 1 &&
+                         M <= 64 && (uintptr_t)x % 16 == 0 && (uintptr_t)w % 16 == 0 &&
+                         (uintptr_t)scales % 4 == 0 && (uintptr_t)biases % 4 == 0 && 64 * K * 2 < ((int64_t)1 << 31) &&
+                         N * K / 2 < ((int64_t)1 << 31) && bm.n_w * N * (K / group_size) * 2 < ((int64_t)1 << 31) &&
+                         bm.seg == nullptr;
+  if (stream_ok) {
+    if (dtype == MLXQ_BFLOAT16)
+      return group_size == 64 ? launch_qmm_stream<BF16, 64>(x, batch, M, K, w, scales, biases, bm, N, y, s)
+                              : launch_qmm_stream<BF16, 128>(x, batch, M, K, w, scales, biases, bm, N, y, s);
+    return group_size == 64 ? launch_qmm_stream<F16, 64>(x, batch, M, K, w, scales, biases, bm, N, y, s)
+                            : launch_qmm_stream<F16, 128>(x, batch, M, K, w, scales, biases, bm, N, y, s);
   }
 
   const bool tile_ok = transpose && mlxq::is_half_dtype(dtype) && (bits == 4 || bits == 8) && K % 64 == 0 &&

@@ -89,6 +89,24 @@ def test_qmm_mfma_variants(O, mlxq_dev, dtype, bits, gs, M, N, K):
     assert_close(y, x.astype(np.float64) @ deq64(O, *wq, gs, bits, dtype).T, what="mfma variant", dtype=dtype)
 
 
+@pytest.mark.parametrize("force,dtype,gs,M,N,K", [
+    ("2", BF16, 64, 64, 14336, 4096),   # up projection, no K split
+    ("2", BF16, 64, 64, 4096, 14336),   # down projection, K split
+    ("2", F16, 128, 17, 200, 1280),     # two row blocks, ragged N, 10 K tiles (chunk past the end)
+    ("2", BF16, 128, 48, 96, 384),      # three row blocks, 3 K tiles (less than one chunk)
+    ("1", BF16, 64, 5, 130, 2048),      # M <= 16 routed away from qmv
+])
+def test_qmm_stream_kernel(O, mlxq_dev, monkeypatch, force, dtype, gs, M, N, K):
+    """The streaming kernel (opt-in through MLXQ_QMM_STREAM) against the same
+    reference: ragged N, partial chunks, both group sizes and dtypes."""
+    monkeypatch.setenv("MLXQ_QMM_STREAM", force)
+    w = rng_t(O, (N, K), 7, dtype, 0.05)
+    wq = O.quantize(w, gs, 4, dtype)
+    x = rng_t(O, (M, K), 8, dtype)
+    y = run_qmm(O, mlxq_dev, x, wq, gs, 4, dtype)
+    assert_close(y, x.astype(np.float64) @ deq64(O, *wq, gs, 4, dtype).T, what="stream", dtype=dtype)
+
+
 @pytest.mark.parametrize("dtype,bits,gs,transpose", [
     (BF16, 4, 64, False), (F16, 8, 32, False), (BF16, 2, 64, True), (F32, 4, 64, True), (BF16, 4, 32, True)])
 def test_qmm_generic_paths(O, mlxq_dev, dtype, bits, gs, transpose):
