@@ -21,10 +21,12 @@
 // without a branch) and reduce their partial rows in LDS (fixed order, no
 // cross-workgroup traffic).
 //
-// Larger M (or K too long for qmv's x slices) takes the tiled MFMA GEMM;
-// everything else (transpose = false, 2-bit, fp32 activations) the VALU
-// kernel below.  All three resolve a batch element through a BatchMap, which
-// also serves mx.gather_qmm (an x row map and an expert index per element).
+// M <= 64 at 4 bits, group 64 (the shapes qmv does not take) runs the
+// direct-to-LDS pipelined MFMA GEMM; larger M, other groups and 8-bit take
+// the tiled MFMA GEMM; everything else (transpose = false, 2-bit, fp32
+// activations) the VALU kernel below.  All of them resolve a batch element
+// through a BatchMap, which also serves mx.gather_qmm (an x row map and an
+// expert index per element).
 #include <algorithm>
 #include <cstdlib>
 
@@ -303,64 +305,113 @@ __global__ void __launch_bounds__(512) qmv_kernel(const uint16_t* __restrict__ x
   }
 }
 
-// ---- streaming MFMA GEMM for 8 < M <= 64 (4-bit, transpose = true) -------
+// ---- direct-to-LDS pipelined MFMA GEMM for 16 < M <= 64 (4-bit, group 64) --
 //
-// A workgroup owns R = 4 weight row tiles (64 rows) and a range of 128-code
-// K tiles, for all M activation rows (MB = ceil(M / 16) MFMA row blocks), so
-// each weight operand serves all of M and each x operand every row tile of
-// its consumer.  Its 12 waves split the work:
-//   * waves 8..11 (producers) stage x through LDS in chunks of 4 K tiles
-//     (double buffered, pre-permuted into the code slot order); their loads
-//     come from L2 (every workgroup reads all of x);
-//   * waves 0..7 (consumers, two per SIMD so one's MFMAs cover the other's
-//     LDS reads and fold) take K tile w % 4 of each chunk for row tiles
-//     2 (w / 4) and 2 (w / 4) + 1: its weights (one dwordx4 per lane per row
-//     tile, 16 rows x 64 contiguous bytes, then a 4 x 4 dword transpose across
-//     the lane quarters so k-step j holds codes 32 j .. 32 j + 31 and never
-//     leaves a quantization group), scales and biases stream PF chunks ahead
-//     through registers; per group X = x against ones (row sums) and D = x
-//     against the exact code operands fold as acc += s D + (b - OFF s) X.
-// Only the consumers' queues hold the weight stream and only the producers'
-// the x loads, so neither waits for the other's loads (vector loads complete
-// in order); one LDS-only barrier per chunk hands the buffers over.  The
-// consumers' accumulators are summed in LDS in fixed order; workgroups of a
-// K split (blockIdx.z = batch * KS + split) write fp32 partials for
-// qmm_splitk_reduce_kernel.  Rows past M or N read zeros and are not stored.
-template <int MB, int NC_>
-struct StreamShape {
-  static constexpr int R = 4;            // weight row tiles per workgroup
-  static constexpr int C = 4;            // K tiles per chunk
-  static constexpr int NC = NC_;         // consumer waves: K tile (w % C), row tiles RC (w / C) ..
-  static constexpr int RC = R * C / NC;  // row tiles per consumer
-  static constexpr int NP = 4;           // producer waves
-  static constexpr int NT = 64 * (NC + NP);
-  static constexpr int CK = C * 128;     // codes (x values) per chunk row
-  static constexpr int BLOCKS = MB * C * 4;                 // 1 KB operand blocks per chunk
-  static constexpr int XBUF = BLOCKS * 1024;                // bytes per x buffer
-  static constexpr int RED = NC * RC * MB * 64 * 16;        // consumer reduction
-  static constexpr int LDS = 2 * XBUF > RED ? 2 * XBUF : RED;
-  static constexpr int BPW = BLOCKS / NP;                   // blocks per producer wave
-  static_assert(BLOCKS % NP == 0 && RC >= 1, "work split");
+// A workgroup owns 64 weight rows (4 row tiles) and a range of 128-code K
+// tiles, for all M activation rows (MB = ceil(M / 16) MFMA row blocks).  One
+// K tile per pipeline step.  Its operands reach LDS through direct-to-LDS
+// buffer loads (buffer_load_dwordx4 ... lds: each lane's 16 bytes land at
+// base + 16 lane), so nothing in flight occupies registers and the rings can
+// be deep:
+//   * weight ring, NSW slots: the tile's 4 x 1 KB of codes (16 rows x 64
+//     bytes per load: piece q of row n at (16 q + n) 16 bytes, so k-step q's
+//     MFMA operand is one 4-byte LDS read per lane); the codes go out WB = 4
+//     tiles at a time, each with the 64 rows' scales and biases of its 4
+//     tiles (16 bytes a row: a 4-byte load per row and tile would touch 64
+//     lines for 256 bytes);
+//   * x ring, NSX slots: the MB x 4 A operand blocks (1 KB each, lane l =
+//     row l % 16, x values 8 (l / 16) .. + 8 of the k-step, natural order).
+// Waves 0..3 issue the weight loads (row tile w; wave 0 also the scales,
+// wave 1 the biases), waves 4..7 the x loads (k-step w - 4 of every row
+// block): a wave waits only for its own loads (vector memory counts complete
+// in order per wave), so the x stream, which comes from L2, never waits
+// behind the weight stream from HBM.  Per step every wave waits for its
+// loads of the step, one barrier publishes the step and frees the slots of
+// the one before, and the next loads go out (x: the step NSX - 1 ahead;
+// weights, at a batch's first step: the batch NSB - 1 ahead).
+// Every wave computes: wave w takes row tile w % 4 and group w / 4 of the K
+// tile (two k-steps) for all MB row blocks: X = x against ones and D = x
+// against the exact codes (natural slot order: (128 or 1024) + c), folded as
+// acc += s D + (b - OFF s) X.  The two group halves are summed in LDS in
+// fixed order; K splits (blockIdx.z = batch * KS + split) write fp32
+// partials for qmm_splitk_reduce_kernel.  Rows past M or N read zeros (the
+// descriptors end there) and are not stored; steps past the split's end load
+// nothing (offsets past the descriptors), so every wave issues the same
+// count each step and its wait counts stay exact.
+template <int MB>
+struct DmaShape {
+  static constexpr int WB = 4;                                  // K tiles per weight batch
+  static constexpr int NSW = MB >= 3 ? 12 : MB == 2 ? 16 : 20;  // weight ring slots (K tiles)
+  static constexpr int NSB = NSW / WB;                          // scale ring slots (batches)
+  static constexpr int NSX = MB == 4 ? 6 : 8;                   // x ring slots (K tiles)
+  static constexpr int WSLOT = 4 * 1024;                        // codes of a K tile
+  static constexpr int SSLOT = 2 * 1024;                        // scales, biases of a batch
+  static constexpr int XSLOT = MB * 4 * 1024;                   // x operand blocks of a K tile
+  static constexpr int SOFF = NSW * WSLOT;
+  static constexpr int XOFF = SOFF + NSB * SSLOT;
+  static constexpr int LDS = XOFF + NSX * XSLOT;
+  static constexpr int RED = 8 * MB * 64 * 16;                  // per-wave accumulators at the end
+  // Loads a weight wave issues per batch: (waves 0, 1) the batch's scales
+  // or biases, then its row tile's codes of the WB tiles.  At step
+  // c = WB k + p it waits before any issue of that step: batches up to
+  // k + NSB - 2 are out at p = 0, up to k + NSB - 1 at p > 0, so after the
+  // codes of step c went out WB - 1 - p codes of batch k and (NSB - 2),
+  // resp. (NSB - 1), whole batches; the wait also covers batch k's scales,
+  // issued before its codes.
+  template <int LB>
+  static constexpr int wait_w(int p) {
+    return (WB - 1 - p) + (p == 0 ? NSB - 2 : NSB - 1) * LB;
+  }
+  static constexpr int WAIT_X = (NSX - 2) * MB;  // x waves: MB blocks a step, NSX - 2 steps after c
+  static_assert(LDS <= 160 * 1024 && RED <= LDS, "LDS budget");
+  static_assert(NSW % WB == 0 && NSB >= 2 && wait_w<5>(1) <= 63 && WAIT_X <= 63, "ring / vmcnt range");
 };
 
-template <typename T, int GS, int MB, int NC_, int PF>
-__global__ void __launch_bounds__(64 * (NC_ + 4)) qmm_stream_kernel(const uint16_t* __restrict__ x, int M, int K,
-                                                         const uint32_t* __restrict__ w,
-                                                         const uint16_t* __restrict__ scales,
-                                                         const uint16_t* __restrict__ biases, int N, BatchMap bm,
-                                                         int KS, int KTS, uint16_t* __restrict__ y,
-                                                         float* __restrict__ part) {
-  using SH = StreamShape<MB, NC_>;
-  static_assert(SH::NT == 64 * (NC_ + 4), "launch bounds");
-  using CO = CodeOps<T, 4>;
-  constexpr int R = SH::R, C = SH::C, BPW = SH::BPW, NC = SH::NC, RC = SH::RC;
-  constexpr int NG = 128 / GS;  // quantization groups per K tile (1 or 2)
-  constexpr int KPG = GS / 32;  // k-steps per group
-  constexpr float OFF = CO::OFFSET;
-  static_assert(GS == 64 || GS == 128, "group size");
-  // x chunks in LDS in MFMA operand order: block (b, kt, j) of buffer p is
-  // the A operand of row block b, K tile kt of the chunk, k-step j (1 KB,
-  // 16 bytes a lane, lane l = row l % 16, x values 8 (l / 16) .. + 8)
+// s_waitcnt vmcnt(N) alone (expcnt and lgkmcnt left at their maxima)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N <= 63, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// s_barrier that also keeps the compiler from moving memory accesses across
+// it.  Unlike a release fence on LDS it does not make the compiler wait for
+// the direct-to-LDS loads in flight (those are tracked by vmcnt and waited
+// for explicitly before it).
+__device__ __forceinline__ void dma_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+__device__ __forceinline__ void dma_load16(__amdgpu_buffer_rsrc_t r, const void* lds, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(uintptr_t)lds, 16, voff, 0, 0,
+                                           0);
+}
+// MFMA B operand from 8 4-bit codes in natural slot order: dword t holds
+// (OFF + c_2t, OFF + c_2t+1), OFF + c being exact in T (bf16 128 + c =
+// 0x4300 + c, f16 1024 + c = 0x6400 + c: the code is the low byte)
+template <typename T>
+__device__ __forceinline__ u32x4_t nat_operand(uint32_t w) {
+  constexpr uint32_t HI = std::is_same<T, BF16>::value ? 0x43434343u : 0x64646464u;
+  const uint32_t lo = w & 0x0f0f0f0fu;         // c0 c2 c4 c6
+  const uint32_t hi = (w >> 4) & 0x0f0f0f0fu;  // c1 c3 c5 c7
+  const uint32_t p = perm_b32(hi, lo, 0x05010400u);  // c0 c1 c2 c3
+  const uint32_t q = perm_b32(hi, lo, 0x07030602u);  // c4 c5 c6 c7
+  u32x4_t r;
+  r.x = perm_b32(HI, p, 0x04010400u);
+  r.y = perm_b32(HI, p, 0x04030402u);
+  r.z = perm_b32(HI, q, 0x04010400u);
+  r.w = perm_b32(HI, q, 0x04030402u);
+  return r;
+}
+
+template <typename T, int MB>
+__global__ void __launch_bounds__(512) qmm_dma_kernel(const uint16_t* __restrict__ x, int M, int K,
+                                                      const uint32_t* __restrict__ w,
+                                                      const uint16_t* __restrict__ scales,
+                                                      const uint16_t* __restrict__ biases, int N, BatchMap bm, int KS,
+                                                      int KTS, uint16_t* __restrict__ y, float* __restrict__ part) {
+  using SH = DmaShape<MB>;
+  constexpr int NSW = SH::NSW, NSX = SH::NSX;
+  constexpr float OFF = Mma<T>::MAGIC_VAL;
+  constexpr uint32_t OOB = 0x80000000u;
   extern __shared__ __align__(16) uint8_t smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -369,270 +420,148 @@ __global__ void __launch_bounds__(64 * (NC_ + 4)) qmm_stream_kernel(const uint16
   int64_t xb, wb;
   bool xok, wok;
   bm.resolve(bidx, xb, xok, wb, wok);
-  const int n0 = blockIdx.x * 16 * R;
-  const int nrows = wok ? min(16 * R, N - n0) : 0;
-  const int G = K / GS, KT = K / 128;
+  const int n0 = blockIdx.x * 64;
+  const int nrows = wok ? min(64, N - n0) : 0;
+  const int G = K / 64, KT = K / 128;
   const int sk0 = split * KTS, sk1 = min(KT, sk0 + KTS);
-  const int nch = (sk1 - sk0 + C - 1) / C;  // chunks of this workgroup
-  // the consumers' chunk loop runs a multiple of PF chunks with no branch
-  // around its loads (so the waits before a chunk leave the later chunks'
-  // loads in flight); chunks past nch compute with zero scales (adding 0)
-  const int ncp = (nch + PF - 1) / PF * PF;
+  const int nch = max(sk1 - sk0, 0);
   const uint32_t row_bytes = (uint32_t)K / 2;
-  // workgroups start at different chunks (in order of their launch on one
-  // XCD, blockIdx.x / 8), so the XCD's workgroups do not all read the same x
-  // lines at once; chunk c of the loop is chunk phys(c) of the split
-  const int spread = nch > 0 ? 1 << (31 - __builtin_clz(nch)) : 1;  // largest power of 2 <= nch
-  const int rot = (int)((blockIdx.x >> 3) + blockIdx.z) & (spread - 1);
-  // (past nch: any chunk; those loads are clamped and their terms zeroed)
-  auto phys = [&](int c) {
-    const int q = c + rot;
-    return q >= nch ? q - nch : q;
-  };
+  const __amdgpu_buffer_rsrc_t rw =
+      make_rsrc(w + ((int64_t)wb * N + n0) * (row_bytes / 4), (uint32_t)nrows * row_bytes);
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(scales + ((int64_t)wb * N + n0) * G, (uint32_t)nrows * (uint32_t)G * 2u);
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(biases + ((int64_t)wb * N + n0) * G, (uint32_t)nrows * (uint32_t)G * 2u);
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + xb * M * K, xok ? (uint32_t)M * (uint32_t)K * 2u : 0u);
+  uint8_t* const xring = smem + SH::XOFF;
 
-  if (wave >= NC) {
-    // ---------------------------------------------------------- producers
-    // producer wave pw stages k-step pw of every (row block, K tile) of each
-    // chunk: lane l loads x row 16 b + l % 16, values 8 (l / 16) .. + 8 of
-    // the k-step (64 bytes of each of 16 rows per load, from L2)
-    static_assert(SH::NP == 4 && BPW == MB * C, "one k-step per producer wave");
-    const int pw = wave - NC;
-    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + xb * M * K, xok ? (uint32_t)M * (uint32_t)K * 2u : 0u);
-    uint32_t vrow[MB];  // row part of each row block's offsets (rows past M: past the descriptor)
+  // Batch k = steps WB k .. WB k + WB - 1 covers K tiles tile0(k) .. + WB - 1
+  // of the split.  With whole batches only, the workgroups of one XCD
+  // (blockIdx.x / 8 consecutive) start at different batches, so they do not
+  // all read the same x lines at once.
+  constexpr int WB = SH::WB, NSB = SH::NSB;
+  const int nb = (nch + WB - 1) / WB;
+  const int spread = nch % WB == 0 && nb > 0 ? 1 << (31 - __builtin_clz(nb)) : 1;  // power of 2 <= nb
+  const int rot = (int)((blockIdx.x >> 3) + blockIdx.z) & (spread - 1);
+  auto tile0 = [&](int k) {  // (past nb: any tile; those loads are masked)
+    const int q = k + rot;
+    return sk0 + WB * (q >= nb ? q - nb : q);
+  };
+  // the batch's 16-byte scale / bias load covers tiles sload(k) .. + 3 of
+  // every row: the batch's own, shifted back to stay inside the row
+  auto sload = [&](int k) { return min(tile0(k), KT - WB); };
+  // waves 0..3: codes of row tile `wave` (lane: row ln, piece lq)
+  const uint32_t voff_w = (uint32_t)(16 * wave + ln) * row_bytes + 16u * lq;
+  // waves 0, 1: scales / biases (lane: row `lane`, 4 tiles' 8 groups)
+  const uint32_t voff_sb = (uint32_t)lane * (uint32_t)G * 2u;
+  // waves 4..7: k-step wave - 4 of row block b (lane: row 16 b + ln, values 8 lq ..)
+  const uint32_t voff_x = (uint32_t)ln * (uint32_t)K * 2u + (uint32_t)(32 * (wave - 4) + 8 * lq) * 2u;
+  auto issue_w = [&](int k) {  // batch k, weight waves: scales / biases first, then the codes
+    const int t0 = tile0(k);
+    if (wave < 2)
+      dma_load16(wave == 0 ? rs : rb, smem + SH::SOFF + (k % NSB) * SH::SSLOT + wave * 1024,
+                 WB * k < nch ? voff_sb + (uint32_t)sload(k) * 4u : OOB);
+#pragma unroll
+    for (int p = 0; p < WB; p++) {
+      const int c = WB * k + p;
+      dma_load16(rw, smem + (c % NSW) * SH::WSLOT + wave * 1024,
+                 c < nch ? voff_w + (uint32_t)(t0 + p) * 64u : OOB);
+    }
+  };
+  auto issue_x = [&](int c) {  // step c, x waves
+    const int kt = tile0(c / WB) + c % WB;
+    uint8_t* slot = xring + (c % NSX) * SH::XSLOT;
 #pragma unroll
     for (int b = 0; b < MB; b++)
-      vrow[b] = 16 * b + ln < M ? (uint32_t)(16 * b + ln) * (uint32_t)K * 2u + 16u * lq : 0x80000000u;
-    // two register buffers: chunk c is staged from one, which then takes
-    // chunk c + 2's loads, so two chunks stay in flight across the barriers
-    // (a chunk past nch reads zeros: every offset is pushed past the
-    // descriptor; staging them is harmless, the consumers give those chunks
-    // zero scales).  Where the registers do not fit beside the consumers'
-    // (8 consumers at MB = 4) one buffer is loaded and staged per chunk.
-    constexpr bool XDB = NC == 4 || MB <= 3;
-    u32x4_t xr[XDB ? 2 : 1][BPW];
-    auto load = [&](u32x4_t (&v)[BPW], int c) {
-#pragma unroll
-      for (int i = 0; i < BPW; i++) {
-        const int kt = sk0 + phys(c) * C + i % C;  // workgroup-uniform
-        const bool ok = (c < nch) & (kt < sk1);
-        const uint32_t col = (uint32_t)(kt * 128 + pw * 32) * 2u;
-        v[i] = buf_load128(rx, ok ? vrow[i / C] + col : 0x80000000u, 0u);
+      dma_load16(rx, slot + (b * 4 + (wave - 4)) * 1024,
+                 c < nch ? voff_x + (uint32_t)(16 * b) * (uint32_t)K * 2u + (uint32_t)kt * 256u : OOB);
+  };
+  auto wait_w = [&](int p) {
+    if (wave < 2) {
+      switch (p) {
+        case 0: wait_vmcnt<SH::template wait_w<WB + 1>(0)>(); break;
+        case 1: wait_vmcnt<SH::template wait_w<WB + 1>(1)>(); break;
+        case 2: wait_vmcnt<SH::template wait_w<WB + 1>(2)>(); break;
+        default: wait_vmcnt<SH::template wait_w<WB + 1>(3)>(); break;
       }
-    };
-    auto stage = [&](const u32x4_t (&v)[BPW], int c) {
-      uint8_t* dst = smem + (c & 1) * SH::XBUF + (pw * 64 + lane) * 16;
-#pragma unroll
-      for (int i = 0; i < BPW; i++)  // block (i / C, i % C, pw)
-        *reinterpret_cast<u32x4_t*>(dst + i * 4096) = permute8<CO::ORDER>(v[i]);
-    };
-    if constexpr (XDB) {
-      static_assert(PF % 2 == 0, "ncp is a multiple of PF: the pair loop needs it even");
-      // no branch in the loop body (a split body lets the allocator rotate
-      // the buffers, and the copies back would wait for the newest loads)
-      load(xr[0], 0);
-      __builtin_amdgcn_sched_barrier(0);
-      load(xr[1], 1);
-      __builtin_amdgcn_sched_barrier(0);
-      for (int c = 0; c < ncp; c += 2) {
-        stage(xr[0], c);
-        __builtin_amdgcn_sched_barrier(0);
-        load(xr[0], c + 2);
-        __builtin_amdgcn_sched_barrier(0);
-        lds_barrier();  // B_c: chunk c staged / consumers done with chunk c - 1
-        stage(xr[1], c + 1);
-        __builtin_amdgcn_sched_barrier(0);
-        load(xr[1], c + 3);
-        __builtin_amdgcn_sched_barrier(0);
-        lds_barrier();  // B_{c+1}
-      }
-      lds_barrier();  // B_ncp
     } else {
-      for (int c = 0; c <= ncp; c++) {
-        if (c < nch) {  // workgroup-uniform
-          load(xr[0], c);
-          stage(xr[0], c);
-        }
-        lds_barrier();  // B_c
+      switch (p) {
+        case 0: wait_vmcnt<SH::template wait_w<WB>(0)>(); break;
+        case 1: wait_vmcnt<SH::template wait_w<WB>(1)>(); break;
+        case 2: wait_vmcnt<SH::template wait_w<WB>(2)>(); break;
+        default: wait_vmcnt<SH::template wait_w<WB>(3)>(); break;
       }
     }
-  } else {
-    // ---------------------------------------------------------- consumers
-    const int kslot = wave % C, rgrp = wave / C;  // K tile of each chunk, row tiles RC rgrp ..
-    const __amdgpu_buffer_rsrc_t rw =
-        make_rsrc(w + ((int64_t)wb * N + n0) * (row_bytes / 4), (uint32_t)nrows * row_bytes);
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(scales + ((int64_t)wb * N + n0) * G, (uint32_t)nrows * (uint32_t)G * 2u);
-    const __amdgpu_buffer_rsrc_t rb = make_rsrc(biases + ((int64_t)wb * N + n0) * G, (uint32_t)nrows * (uint32_t)G * 2u);
-    uint32_t wlane[RC], slane[RC];
+  };
+  static_assert(WB == 4, "wait_w phases");
+
+  const int rt = wave & 3, kg = wave >> 2;  // compute: row tile, group of the K tile
+  f32x4_t acc[MB];
 #pragma unroll
-    for (int r = 0; r < RC; r++) {
-      const int row = ln + 16 * (RC * rgrp + r);
-      wlane[r] = (uint32_t)row * row_bytes + 16u * lq;
-      slane[r] = (uint32_t)row * (uint32_t)G * 2u;
+  for (int b = 0; b < MB; b++) acc[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const u32x4_t ones = {Mma<T>::ONES, Mma<T>::ONES, Mma<T>::ONES, Mma<T>::ONES};
+
+  if (wave < 4)
+    for (int k = 0; k < NSB - 1; k++) issue_w(k);
+  else
+    for (int c = 0; c < NSX - 1; c++) issue_x(c);
+  for (int c = 0; c < nch; c++) {
+    const int k = c / WB, p = c % WB;
+    if (wave < 4)
+      wait_w(p);
+    else
+      wait_vmcnt<SH::WAIT_X>();
+    dma_barrier();  // step c in LDS everywhere; the slots of steps before c free
+    if (wave >= 4)
+      issue_x(c + NSX - 1);
+    else if (p == 0)
+      issue_w(k + NSB - 1);
+    const uint8_t* ws = smem + (c % NSW) * SH::WSLOT;
+    const uint8_t* xs = xring + (c % NSX) * SH::XSLOT;
+    // (s, b) of group 2 kt + kg of row 16 rt + ln: halfword 2 (kt - sload) + kg
+    // of the row's 16 bytes
+    const uint8_t* ss = smem + SH::SOFF + (k % NSB) * SH::SSLOT + (16 * rt + ln) * 16 +
+                        (2 * (tile0(k) + p - sload(k)) + kg) * 2;
+    const float sc = Conv<T>::from_bits(*reinterpret_cast<const uint16_t*>(ss));
+    const float bp = Conv<T>::from_bits(*reinterpret_cast<const uint16_t*>(ss + 1024)) - OFF * sc;
+    f32x4_t X[MB], D[MB];
+#pragma unroll
+    for (int b = 0; b < MB; b++) {
+      X[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      D[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
-    u32x4_t wr[PF][RC];
-    uint32_t sr[PF][RC], br[PF][RC];
-    // this consumer's K tile of chunk c (past the split's end: the last one
-    // re-read, its contribution zeroed below)
-    auto issue = [&](int slot, int c) {
-      const int kt = min(sk0 + phys(c) * C + kslot, sk1 - 1);
-      const uint32_t woff = (uint32_t)kt * 64u;
-      // GS 64: the dword of groups 2 kt, 2 kt + 1 (4-byte aligned, G even);
-      // GS 128: the one 16-bit group kt (a dword there could cross the end
-      // of the descriptor when G is odd, and would then read as zero)
-      const uint32_t soff = (uint32_t)(kt * NG) * 2u;
 #pragma unroll
-      for (int r = 0; r < RC; r++) wr[slot][r] = buf_load128(rw, wlane[r], woff);
+    for (int jj = 0; jj < 2; jj++) {
+      const int j = 2 * kg + jj;
+      const u32x4_t bop =
+          nat_operand<T>(*reinterpret_cast<const uint32_t*>(ws + rt * 1024 + (16 * j + ln) * 16 + 4 * lq));
 #pragma unroll
-      for (int r = 0; r < RC; r++) {
-        sr[slot][r] = NG == 2 ? buf_load32(rs, slane[r], soff) : buf_load16(rs, slane[r], soff);
-        br[slot][r] = NG == 2 ? buf_load32(rb, slane[r], soff) : buf_load16(rb, slane[r], soff);
-      }
-    };
-    f32x4_t acc[RC][MB];
-#pragma unroll
-    for (int r = 0; r < RC; r++)
-#pragma unroll
-      for (int b = 0; b < MB; b++) acc[r][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    const u32x4_t ones = {Mma<T>::ONES, Mma<T>::ONES, Mma<T>::ONES, Mma<T>::ONES};
-    const uint32_t magic = opaque(Mma<T>::MAGIC);
-    // slot order is issue order (the scheduler may not interleave slots: a
-    // load of slot 0 issued after slot 1's would make every wait for slot 0
-    // wait for slot 1 too)
-#pragma unroll
-    for (int p = 0; p < PF; p++) {
-      issue(p, p);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    lds_barrier();  // B_0
-    for (int cb = 0; cb < ncp; cb += PF) {
-#pragma unroll
-      for (int p = 0; p < PF; p++) {
-        const int c = cb + p;
-        const bool live = (c < nch) & (sk0 + phys(c) * C + kslot < sk1);  // no branch in the loop body
-        uint32_t wt[RC][4];
-#pragma unroll
-        for (int r = 0; r < RC; r++) {
-          wt[r][0] = wr[p][r].x;
-          wt[r][1] = wr[p][r].y;
-          wt[r][2] = wr[p][r].z;
-          wt[r][3] = wr[p][r].w;
-          quarter_transpose(wt[r]);
-        }
-        float s_g[RC][NG], b_g[RC][NG];
-#pragma unroll
-        for (int r = 0; r < RC; r++) {
-#pragma unroll
-          for (int gi = 0; gi < NG; gi++) {
-            // GS 64: groups 2 kt (low half), 2 kt + 1 (high); GS 128: group kt
-            const int sh = 16 * gi;
-            const float sc = Conv<T>::from_bits((sr[p][r] >> sh) & 0xffffu);
-            const float bi = Conv<T>::from_bits((br[p][r] >> sh) & 0xffffu);
-            s_g[r][gi] = live ? sc : 0.f;
-            b_g[r][gi] = live ? bi - OFF * sc : 0.f;
-          }
-        }
-        const uint8_t* xc = smem + (c & 1) * SH::XBUF + kslot * 4096 + lane * 16;
-        // per group: X[b] = x against ones, D = x against the codes; the
-        // loop order keeps the fewer registers live (all k-steps' x operands
-        // with one row tile's D, or one k-step's with every row tile's D)
-        constexpr bool BY_STEP = RC <= KPG;
-#pragma unroll
-        for (int gi = 0; gi < NG; gi++) {
-          f32x4_t X[MB];
-#pragma unroll
-          for (int b = 0; b < MB; b++) X[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-          auto fold = [&](int r, const f32x4_t (&Dr)[MB]) {
-#pragma unroll
-            for (int b = 0; b < MB; b++)
-#pragma unroll
-              for (int i = 0; i < 4; i++)
-                acc[r][b][i] =
-                    __builtin_fmaf(s_g[r][gi], Dr[b][i], __builtin_fmaf(b_g[r][gi], X[b][i], acc[r][b][i]));
-          };
-          auto xop = [&](int b, int j) {
-            return *reinterpret_cast<const u32x4_t*>(xc + (b * C * 4 + gi * KPG + j) * 1024);
-          };
-          if constexpr (BY_STEP) {
-            f32x4_t D[RC][MB];
-#pragma unroll
-            for (int r = 0; r < RC; r++)
-#pragma unroll
-              for (int b = 0; b < MB; b++) D[r][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int j = 0; j < KPG; j++) {
-              u32x4_t a[MB];
-#pragma unroll
-              for (int b = 0; b < MB; b++) {
-                a[b] = xop(b, j);
-                X[b] = Mma<T>::mma(a[b], ones, X[b]);
-              }
-#pragma unroll
-              for (int r = 0; r < RC; r++) {
-                const u32x4_t bop = CO::operand(wt[r][gi * KPG + j], magic);
-#pragma unroll
-                for (int b = 0; b < MB; b++) D[r][b] = Mma<T>::mma(a[b], bop, D[r][b]);
-              }
-            }
-#pragma unroll
-            for (int r = 0; r < RC; r++) fold(r, D[r]);
-          } else {
-            u32x4_t a[MB][KPG];
-#pragma unroll
-            for (int b = 0; b < MB; b++)
-#pragma unroll
-              for (int j = 0; j < KPG; j++) {
-                a[b][j] = xop(b, j);
-                X[b] = Mma<T>::mma(a[b][j], ones, X[b]);
-              }
-#pragma unroll
-            for (int r = 0; r < RC; r++) {
-              f32x4_t D[MB];
-#pragma unroll
-              for (int b = 0; b < MB; b++) D[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-              for (int j = 0; j < KPG; j++) {
-                const u32x4_t bop = CO::operand(wt[r][gi * KPG + j], magic);
-#pragma unroll
-                for (int b = 0; b < MB; b++) D[b] = Mma<T>::mma(a[b][j], bop, D[b]);
-              }
-              fold(r, D);
-            }
-          }
-        }
-        // chunk c + PF's loads go into this slot once its weights are dead
-        // (issued earlier, their registers would overlap the transposed
-        // weights still in use, the allocator would rotate the slots and
-        // the copies back at the loop end would wait for the new loads)
-        __builtin_amdgcn_sched_barrier(0);
-        issue(p, c + PF);
-        __builtin_amdgcn_sched_barrier(0);
-        lds_barrier();  // B_{c+1}
+      for (int b = 0; b < MB; b++) {
+        const u32x4_t a = *reinterpret_cast<const u32x4_t*>(xs + (b * 4 + j) * 1024 + lane * 16);
+        X[b] = Mma<T>::mma(a, ones, X[b]);
+        D[b] = Mma<T>::mma(a, bop, D[b]);
       }
     }
-    // the x buffers are free after the last barrier: sum the consumers there
-    f32x4_t* red = reinterpret_cast<f32x4_t*>(smem);  // [NC][RC * MB][64]
 #pragma unroll
-    for (int r = 0; r < RC; r++)
+    for (int b = 0; b < MB; b++)
 #pragma unroll
-      for (int b = 0; b < MB; b++) red[(wave * RC * MB + r * MB + b) * 64 + lane] = acc[r][b];
+      for (int i = 0; i < 4; i++) acc[b][i] = __builtin_fmaf(sc, D[b][i], __builtin_fmaf(bp, X[b][i], acc[b][i]));
   }
-  lds_barrier();  // every consumer's accumulators are in LDS
-  if (wave >= NC) return;
-  // output block (row tile rt, row block b) is the sum over the C consumers
-  // of row group rt / RC, in K order; NC waves take the R * MB blocks
-  const f32x4_t* red = reinterpret_cast<const f32x4_t*>(smem);
-  for (int ob = wave; ob < R * MB; ob += NC) {
-    const int rt = ob / MB, b = ob % MB, g = rt / RC, r = rt % RC;
-    f32x4_t v = red[((g * C) * RC * MB + r * MB + b) * 64 + lane];
+  // drain the loads past the end (they land in ring slots) before the LDS is reused
+  wait_vmcnt<0>();
+  lds_barrier();
+  f32x4_t* red = reinterpret_cast<f32x4_t*>(smem);  // [wave][MB][64]
 #pragma unroll
-    for (int k = 1; k < C; k++) {
-      const f32x4_t o = red[((g * C + k) * RC * MB + r * MB + b) * 64 + lane];
-      v[0] += o[0];
-      v[1] += o[1];
-      v[2] += o[2];
-      v[3] += o[3];
-    }
-    const int n = n0 + 16 * rt + ln;
+  for (int b = 0; b < MB; b++) red[(wave * MB + b) * 64 + lane] = acc[b];
+  lds_barrier();
+  // output block (row tile t, row block b) = group 0 + group 1 (waves t, t + 4)
+  for (int ob = wave; ob < 4 * MB; ob += 8) {
+    const int t = ob / MB, b = ob % MB;
+    f32x4_t v = red[(t * MB + b) * 64 + lane];
+    const f32x4_t o = red[((t + 4) * MB + b) * 64 + lane];
+    v[0] += o[0];
+    v[1] += o[1];
+    v[2] += o[2];
+    v[3] += o[3];
+    const int n = n0 + 16 * t + ln;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const int m = 16 * b + 4 * lq + i;
@@ -1099,31 +1028,28 @@ int launch_qmm_tile(const void* x, int64_t batch, int64_t M, int64_t K, const ui
   return launch_qmm_tile_inst<T, BITS, GS, 64, 64>(x, batch, M, K, w, scales, biases, bm, N, y, s);
 }
 
-// MLXQ_QMM_STREAM (A/B tuning): unset or 0 keeps the tiled GEMM for
-// 16 < M <= 64 (the streaming kernel does not beat it yet), 2 routes those
-// shapes to the streaming kernel, 1 also M <= 16 instead of qmv
-// (read on every call, so one process can compare the paths)
+// MLXQ_QMM_STREAM=0 (A/B tuning) keeps the tiled GEMM for the shapes the
+// direct-to-LDS kernel takes by default; read on every call, so one process
+// can compare the paths
 int qmm_stream_override() {
   const char* e = getenv("MLXQ_QMM_STREAM");
-  return e ? atoi(e) : 0;
+  return e ? atoi(e) : 1;
 }
 
-template <typename T, int GS, int MB, int NC>
-int launch_qmm_stream_inst(const void* x, int64_t batch, int64_t M, int64_t K, const uint32_t* w,
-                           const void* scales, const void* biases, const BatchMap& bm, int64_t N, void* y,
-                           hipStream_t s) {
-  using SH = StreamShape<MB, NC>;
-  constexpr int PF = 2;
+template <typename T, int MB>
+int launch_qmm_dma_inst(const void* x, int64_t batch, int64_t M, int64_t K, const uint32_t* w, const void* scales,
+                        const void* biases, const BatchMap& bm, int64_t N, void* y, hipStream_t s) {
+  using SH = DmaShape<MB>;
   const int64_t KT = K / 128;
-  const int64_t groups = (N + 16 * SH::R - 1) / (16 * SH::R);
+  const int64_t groups = (N + 63) / 64;
   const int64_t cus = mlxq::device_cu_count();
-  // One workgroup fills a CU (its LDS); split K only when the row groups
+  // One workgroup fills a CU (its LDS).  Split K only when the row groups
   // leave a quarter of the CUs idle, until every CU has one, keeping at
-  // least two chunks per split (each split adds fp32 partial traffic).
+  // least 8 K tiles per split (each split adds fp32 partial traffic).
   int KS = 1;
   const bool can_split = N % 4 == 0 && (uintptr_t)y % 8 == 0;
   if (can_split && 4 * groups * batch < 3 * cus)
-    while (KS < 16 && groups * batch * KS < cus && KT / (KS * 2) >= 2 * SH::C) KS *= 2;
+    while (KS < 16 && groups * batch * KS < cus && KT / (KS * 2) >= 8) KS *= 2;
   const int ov = qmm_ks_override();
   if (ov >= 1 && ov <= 16 && (ov == 1 || can_split)) KS = ov;
   MLXQ_CHECK(batch * KS < 65536, "qmm: batch too large for one launch");
@@ -1136,18 +1062,16 @@ int launch_qmm_stream_inst(const void* x, int64_t batch, int64_t M, int64_t K, c
     part = (float*)p;
   }
   const int KTS = (int)((KT + KS - 1) / KS);
-  auto kern = qmm_stream_kernel<T, GS, MB, NC, PF>;
-  if (SH::LDS > 64 * 1024) {
-    static bool raised = false;  // per instantiation
-    if (!raised) {
-      MLXQ_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, SH::LDS));
-      raised = true;
-    }
+  auto kern = qmm_dma_kernel<T, MB>;
+  static bool raised = false;  // per instantiation
+  if (!raised) {
+    MLXQ_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, SH::LDS));
+    raised = true;
   }
   dim3 grid((unsigned)groups, 1, (unsigned)(batch * KS));
-  hipLaunchKernelGGL(kern, grid, dim3(SH::NT), SH::LDS, s, (const uint16_t*)x, (int)M, (int)K, w,
+  hipLaunchKernelGGL(kern, grid, dim3(512), SH::LDS, s, (const uint16_t*)x, (int)M, (int)K, w,
                      (const uint16_t*)scales, (const uint16_t*)biases, (int)N, bm, KS, KTS, (uint16_t*)y, part);
-  MLXQ_LAUNCHED("qmm_stream_kernel");
+  MLXQ_LAUNCHED("qmm_dma_kernel");
   if (KS > 1) {
     const int64_t n4 = batch * M * N / 4;
     hipLaunchKernelGGL((qmm_splitk_reduce_kernel<T>), dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s,
@@ -1157,14 +1081,14 @@ int launch_qmm_stream_inst(const void* x, int64_t batch, int64_t M, int64_t K, c
   return MLXQ_OK;
 }
 
-template <typename T, int GS>
-int launch_qmm_stream(const void* x, int64_t batch, int64_t M, int64_t K, const uint32_t* w, const void* scales,
-                      const void* biases, const BatchMap& bm, int64_t N, void* y, hipStream_t s) {
+template <typename T>
+int launch_qmm_dma(const void* x, int64_t batch, int64_t M, int64_t K, const uint32_t* w, const void* scales,
+                   const void* biases, const BatchMap& bm, int64_t N, void* y, hipStream_t s) {
   switch ((M + 15) / 16) {
-    case 1: return launch_qmm_stream_inst<T, GS, 1, 8>(x, batch, M, K, w, scales, biases, bm, N, y, s);
-    case 2: return launch_qmm_stream_inst<T, GS, 2, 8>(x, batch, M, K, w, scales, biases, bm, N, y, s);
-    case 3: return launch_qmm_stream_inst<T, GS, 3, 8>(x, batch, M, K, w, scales, biases, bm, N, y, s);
-    default: return launch_qmm_stream_inst<T, GS, 4, 8>(x, batch, M, K, w, scales, biases, bm, N, y, s);
+    case 1: return launch_qmm_dma_inst<T, 1>(x, batch, M, K, w, scales, biases, bm, N, y, s);
+    case 2: return launch_qmm_dma_inst<T, 2>(x, batch, M, K, w, scales, biases, bm, N, y, s);
+    case 3: return launch_qmm_dma_inst<T, 3>(x, batch, M, K, w, scales, biases, bm, N, y, s);
+    default: return launch_qmm_dma_inst<T, 4>(x, batch, M, K, w, scales, biases, bm, N, y, s);
   }
 }
 
@@ -1347,8 +1271,7 @@ int qmm_dispatch(const void* x, int dtype, int64_t batch, int64_t M, int64_t K, 
                       (uintptr_t)w % 16 == 0 && (uintptr_t)scales % 8 == 0 && (uintptr_t)biases % 8 == 0 &&
                       K * M < ((int64_t)1 << 30) && batch < 65536 &&
                       plan_qmv(bits, group_size, M, K, N, batch, &plan);
-  const int sov = qmm_stream_override();
-  if (qmv_ok && !(sov == 1 && bits == 4)) {
+  if (qmv_ok) {
     if (dtype == MLXQ_BFLOAT16) {
       if (bits == 4)
         return group_size == 64 ? launch_qmv<BF16, 4, 64>(x, batch, M, K, w, scales, biases, bm, N, y, plan, s)
@@ -1363,20 +1286,17 @@ int qmm_dispatch(const void* x, int dtype, int64_t batch, int64_t M, int64_t K, 
                             : launch_qmv<F16, 8, 128>(x, batch, M, K, w, scales, biases, bm, N, y, plan, s);
   }
 
-  // 4-bit, 16 < M <= 64 (and M <= 16 when forced): the streaming MFMA GEMM
-  const bool stream_ok = sov >= 1 && (!qmv_ok || sov == 1) && transpose && mlxq::is_half_dtype(dtype) &&
-                         bits == 4 && (group_size == 64 || group_size == 128) && K % 128 == 0 && M >= 1 &&
-                         M <= 64 && (uintptr_t)x % 16 == 0 && (uintptr_t)w % 16 == 0 &&
-                         (uintptr_t)scales % 4 == 0 && (uintptr_t)biases % 4 == 0 && 64 * K * 2 < ((int64_t)1 << 31) &&
-                         N * K / 2 < ((int64_t)1 << 31) && bm.n_w * N * (K / group_size) * 2 < ((int64_t)1 << 31) &&
-                         bm.seg == nullptr;
-  if (stream_ok) {
-    if (dtype == MLXQ_BFLOAT16)
-      return group_size == 64 ? launch_qmm_stream<BF16, 64>(x, batch, M, K, w, scales, biases, bm, N, y, s)
-                              : launch_qmm_stream<BF16, 128>(x, batch, M, K, w, scales, biases, bm, N, y, s);
-    return group_size == 64 ? launch_qmm_stream<F16, 64>(x, batch, M, K, w, scales, biases, bm, N, y, s)
-                            : launch_qmm_stream<F16, 128>(x, batch, M, K, w, scales, biases, bm, N, y, s);
-  }
+  // 4-bit group 64, M <= 64 (the shapes qmv does not take): the
+  // direct-to-LDS pipelined MFMA GEMM
+  const bool dma_ok = qmm_stream_override() != 0 && transpose && mlxq::is_half_dtype(dtype) && bits == 4 &&
+                      group_size == 64 && K % 128 == 0 && K >= 512 && M >= 1 && M <= 64 &&
+                      (uintptr_t)x % 16 == 0 && (uintptr_t)w % 16 == 0 && (uintptr_t)scales % 4 == 0 &&
+                      (uintptr_t)biases % 4 == 0 && 64 * K * 2 < ((int64_t)1 << 31) &&
+                      N * K / 2 < ((int64_t)1 << 31) && bm.n_w * N * (K / group_size) * 2 < ((int64_t)1 << 31) &&
+                      bm.seg == nullptr;
+  if (dma_ok)
+    return dtype == MLXQ_BFLOAT16 ? launch_qmm_dma<BF16>(x, batch, M, K, w, scales, biases, bm, N, y, s)
+                                  : launch_qmm_dma<F16>(x, batch, M, K, w, scales, biases, bm, N, y, s);
 
   const bool tile_ok = transpose && mlxq::is_half_dtype(dtype) && (bits == 4 || bits == 8) && K % 64 == 0 &&
                        (uintptr_t)x % 16 == 0 && (uintptr_t)w % 16 == 0 && (uintptr_t)scales % 4 == 0 &&

@@ -89,22 +89,34 @@ def test_qmm_mfma_variants(O, mlxq_dev, dtype, bits, gs, M, N, K):
     assert_close(y, x.astype(np.float64) @ deq64(O, *wq, gs, bits, dtype).T, what="mfma variant", dtype=dtype)
 
 
-@pytest.mark.parametrize("force,dtype,gs,M,N,K", [
-    ("2", BF16, 64, 64, 14336, 4096),   # up projection, no K split
-    ("2", BF16, 64, 64, 4096, 14336),   # down projection, K split
-    ("2", F16, 128, 17, 200, 1280),     # two row blocks, ragged N, 10 K tiles (chunk past the end)
-    ("2", BF16, 128, 48, 96, 384),      # three row blocks, 3 K tiles (less than one chunk)
-    ("1", BF16, 64, 5, 130, 2048),      # M <= 16 routed away from qmv
+@pytest.mark.parametrize("dtype,M,N,K", [
+    (BF16, 64, 14336, 4096),   # up projection, no K split, rotated batches
+    (BF16, 64, 4096, 14336),   # down projection, K split
+    (F16, 17, 200, 1280),      # two row blocks, ragged N, a partial batch
+    (BF16, 48, 96, 640),       # three row blocks, 5 K tiles (a partial batch)
+    (F16, 32, 64, 1536),       # 12 K tiles: 3 batches, rotated
+    (BF16, 33, 130, 2048),     # ragged M and N
+    (BF16, 16, 4096, 14336),   # one row block (the M = 16 down projection)
 ])
-def test_qmm_stream_kernel(O, mlxq_dev, monkeypatch, force, dtype, gs, M, N, K):
-    """The streaming kernel (opt-in through MLXQ_QMM_STREAM) against the same
-    reference: ragged N, partial chunks, both group sizes and dtypes."""
-    monkeypatch.setenv("MLXQ_QMM_STREAM", force)
+def test_qmm_dma_kernel(O, mlxq_dev, dtype, M, N, K):
+    """The direct-to-LDS pipelined kernel (4-bit, group 64, 16 < M <= 64 and
+    the M <= 16 shapes qmv does not take) against the float64 reference:
+    ragged M and N, partial and rotated batches, both dtypes."""
     w = rng_t(O, (N, K), 7, dtype, 0.05)
-    wq = O.quantize(w, gs, 4, dtype)
+    wq = O.quantize(w, 64, 4, dtype)
     x = rng_t(O, (M, K), 8, dtype)
-    y = run_qmm(O, mlxq_dev, x, wq, gs, 4, dtype)
-    assert_close(y, x.astype(np.float64) @ deq64(O, *wq, gs, 4, dtype).T, what="stream", dtype=dtype)
+    y = run_qmm(O, mlxq_dev, x, wq, 64, 4, dtype)
+    assert_close(y, x.astype(np.float64) @ deq64(O, *wq, 64, 4, dtype).T, what="dma", dtype=dtype)
+
+
+def test_qmm_tile_at_dma_shapes(O, mlxq_dev, monkeypatch):
+    """MLXQ_QMM_STREAM=0 keeps the tiled GEMM reachable at those shapes."""
+    monkeypatch.setenv("MLXQ_QMM_STREAM", "0")
+    w = rng_t(O, (256, 2048), 9, BF16, 0.05)
+    wq = O.quantize(w, 64, 4, BF16)
+    x = rng_t(O, (40, 2048), 10, BF16)
+    y = run_qmm(O, mlxq_dev, x, wq, 64, 4, BF16)
+    assert_close(y, x.astype(np.float64) @ deq64(O, *wq, 64, 4, BF16).T, what="tile", dtype=BF16)
 
 
 @pytest.mark.parametrize("dtype,bits,gs,transpose", [
