@@ -350,21 +350,25 @@ struct DmaShape {
   static constexpr int SOFF = NSW * WSLOT;
   static constexpr int XOFF = SOFF + NSB * SSLOT;
   static constexpr int LDS = XOFF + NSX * XSLOT;
-  static constexpr int RED = 8 * MB * 64 * 16;                  // per-wave accumulators at the end
-  // Loads a weight wave issues per batch: (waves 0, 1) the batch's scales
-  // or biases, then its row tile's codes of the WB tiles.  At step
-  // c = WB k + p it waits before any issue of that step: batches up to
-  // k + NSB - 2 are out at p = 0, up to k + NSB - 1 at p > 0, so after the
-  // codes of step c went out WB - 1 - p codes of batch k and (NSB - 2),
-  // resp. (NSB - 1), whole batches; the wait also covers batch k's scales,
-  // issued before its codes.
+  // The loop runs steps in pairs (c, c + 1), c even; a weight batch is two
+  // pairs.  Loads a weight wave issues per batch: (waves 0, 1) the batch's
+  // scales or biases, then its row tile's codes of the WB tiles.  Before the
+  // pair it waits for step c + 1's codes (which covers step c and the
+  // batch's scales, issued before them): at a batch's first pair, batches up
+  // to k + NSB - 2 are out and 2 codes of batch k follow step c + 1's; at its
+  // second pair batch k + NSB - 1 is out too and none of batch k follow.
   template <int LB>
-  static constexpr int wait_w(int p) {
-    return (WB - 1 - p) + (p == 0 ? NSB - 2 : NSB - 1) * LB;
+  static constexpr int wait_w(bool second) {
+    return second ? (NSB - 1) * LB : 2 + (NSB - 2) * LB;
   }
-  static constexpr int WAIT_X = (NSX - 2) * MB;  // x waves: MB blocks a step, NSX - 2 steps after c
+  // x waves: steps up to c + NSX - 3 are out before the pair (two a pair,
+  // NSX - 2 in the prologue), NSX - 4 steps follow step c + 1's
+  static constexpr int WAIT_X = (NSX - 4) * MB;
+  static constexpr int RED = 8 * 2 * MB * 64 * 16;  // per-wave accumulators at the end
   static_assert(LDS <= 160 * 1024 && RED <= LDS, "LDS budget");
-  static_assert(NSW % WB == 0 && NSB >= 2 && wait_w<5>(1) <= 63 && WAIT_X <= 63, "ring / vmcnt range");
+  static_assert(NSW % WB == 0 && WB == 4 && NSB >= 2 && NSX % 2 == 0 && NSX >= 4 && wait_w<5>(true) <= 63 &&
+                    WAIT_X <= 63,
+                "ring / vmcnt range");
 };
 
 // s_waitcnt vmcnt(N) alone (expcnt and lgkmcnt left at their maxima)
@@ -474,93 +478,116 @@ __global__ void __launch_bounds__(512) qmm_dma_kernel(const uint16_t* __restrict
       dma_load16(rx, slot + (b * 4 + (wave - 4)) * 1024,
                  c < nch ? voff_x + (uint32_t)(16 * b) * (uint32_t)K * 2u + (uint32_t)kt * 256u : OOB);
   };
-  auto wait_w = [&](int p) {
+  auto wait_w = [&](bool second) {
     if (wave < 2) {
-      switch (p) {
-        case 0: wait_vmcnt<SH::template wait_w<WB + 1>(0)>(); break;
-        case 1: wait_vmcnt<SH::template wait_w<WB + 1>(1)>(); break;
-        case 2: wait_vmcnt<SH::template wait_w<WB + 1>(2)>(); break;
-        default: wait_vmcnt<SH::template wait_w<WB + 1>(3)>(); break;
-      }
+      if (second)
+        wait_vmcnt<SH::template wait_w<WB + 1>(true)>();
+      else
+        wait_vmcnt<SH::template wait_w<WB + 1>(false)>();
     } else {
-      switch (p) {
-        case 0: wait_vmcnt<SH::template wait_w<WB>(0)>(); break;
-        case 1: wait_vmcnt<SH::template wait_w<WB>(1)>(); break;
-        case 2: wait_vmcnt<SH::template wait_w<WB>(2)>(); break;
-        default: wait_vmcnt<SH::template wait_w<WB>(3)>(); break;
-      }
+      if (second)
+        wait_vmcnt<SH::template wait_w<WB>(true)>();
+      else
+        wait_vmcnt<SH::template wait_w<WB>(false)>();
     }
   };
-  static_assert(WB == 4, "wait_w phases");
-
-  const int rt = wave & 3, kg = wave >> 2;  // compute: row tile, group of the K tile
-  f32x4_t acc[MB];
+  // compute: of each pair of steps, wave w takes group gi = w % 4 (step
+  // c + gi / 2, group gi % 2 of its tile) for row tiles 2 h, 2 h + 1
+  // (h = w / 4) and every row block: each x operand read serves two row
+  // tiles, each row sum X two D tiles
+  const int gi = wave & 3, h = wave >> 2;
+  f32x4_t acc[2][MB];
 #pragma unroll
-  for (int b = 0; b < MB; b++) acc[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int r = 0; r < 2; r++)
+#pragma unroll
+    for (int b = 0; b < MB; b++) acc[r][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   const u32x4_t ones = {Mma<T>::ONES, Mma<T>::ONES, Mma<T>::ONES, Mma<T>::ONES};
 
   if (wave < 4)
     for (int k = 0; k < NSB - 1; k++) issue_w(k);
   else
-    for (int c = 0; c < NSX - 1; c++) issue_x(c);
-  for (int c = 0; c < nch; c++) {
-    const int k = c / WB, p = c % WB;
+    for (int c = 0; c < NSX - 2; c++) issue_x(c);
+  for (int c = 0; c < nch; c += 2) {
+    const int k = c / WB;
+    const bool second = (c % WB) != 0;
     if (wave < 4)
-      wait_w(p);
+      wait_w(second);
     else
       wait_vmcnt<SH::WAIT_X>();
-    dma_barrier();  // step c in LDS everywhere; the slots of steps before c free
-    if (wave >= 4)
+    dma_barrier();  // steps c, c + 1 in LDS everywhere; the slots of the steps before free
+    if (wave >= 4) {
+      issue_x(c + NSX - 2);
       issue_x(c + NSX - 1);
-    else if (p == 0)
+    } else if (!second) {
       issue_w(k + NSB - 1);
-    const uint8_t* ws = smem + (c % NSW) * SH::WSLOT;
-    const uint8_t* xs = xring + (c % NSX) * SH::XSLOT;
+    }
+    const int st = c + (gi >> 1), kg = gi & 1;
+    if (st >= nch) continue;  // the odd last step (wave-uniform)
+    const uint8_t* ws = smem + (st % NSW) * SH::WSLOT;
+    const uint8_t* xs = xring + (st % NSX) * SH::XSLOT;
     // (s, b) of group 2 kt + kg of row 16 rt + ln: halfword 2 (kt - sload) + kg
     // of the row's 16 bytes
-    const uint8_t* ss = smem + SH::SOFF + (k % NSB) * SH::SSLOT + (16 * rt + ln) * 16 +
-                        (2 * (tile0(k) + p - sload(k)) + kg) * 2;
-    const float sc = Conv<T>::from_bits(*reinterpret_cast<const uint16_t*>(ss));
-    const float bp = Conv<T>::from_bits(*reinterpret_cast<const uint16_t*>(ss + 1024)) - OFF * sc;
-    f32x4_t X[MB], D[MB];
+    float sc[2], bp[2];
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+      const uint8_t* ss = smem + SH::SOFF + (k % NSB) * SH::SSLOT + (16 * (2 * h + r) + ln) * 16 +
+                          (2 * (tile0(k) + st % WB - sload(k)) + kg) * 2;
+      sc[r] = Conv<T>::from_bits(*reinterpret_cast<const uint16_t*>(ss));
+      bp[r] = Conv<T>::from_bits(*reinterpret_cast<const uint16_t*>(ss + 1024)) - OFF * sc[r];
+    }
+    f32x4_t X[MB], D[2][MB];
 #pragma unroll
     for (int b = 0; b < MB; b++) {
       X[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      D[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      D[0][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      D[1][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
 #pragma unroll
     for (int jj = 0; jj < 2; jj++) {
       const int j = 2 * kg + jj;
-      const u32x4_t bop =
-          nat_operand<T>(*reinterpret_cast<const uint32_t*>(ws + rt * 1024 + (16 * j + ln) * 16 + 4 * lq));
+      u32x4_t bop[2];
+#pragma unroll
+      for (int r = 0; r < 2; r++)
+        bop[r] = nat_operand<T>(
+            *reinterpret_cast<const uint32_t*>(ws + (2 * h + r) * 1024 + (16 * j + ln) * 16 + 4 * lq));
 #pragma unroll
       for (int b = 0; b < MB; b++) {
         const u32x4_t a = *reinterpret_cast<const u32x4_t*>(xs + (b * 4 + j) * 1024 + lane * 16);
         X[b] = Mma<T>::mma(a, ones, X[b]);
-        D[b] = Mma<T>::mma(a, bop, D[b]);
+        D[0][b] = Mma<T>::mma(a, bop[0], D[0][b]);
+        D[1][b] = Mma<T>::mma(a, bop[1], D[1][b]);
       }
     }
 #pragma unroll
-    for (int b = 0; b < MB; b++)
+    for (int r = 0; r < 2; r++)
 #pragma unroll
-      for (int i = 0; i < 4; i++) acc[b][i] = __builtin_fmaf(sc, D[b][i], __builtin_fmaf(bp, X[b][i], acc[b][i]));
+      for (int b = 0; b < MB; b++)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          acc[r][b][i] = __builtin_fmaf(sc[r], D[r][b][i], __builtin_fmaf(bp[r], X[b][i], acc[r][b][i]));
   }
   // drain the loads past the end (they land in ring slots) before the LDS is reused
   wait_vmcnt<0>();
   lds_barrier();
-  f32x4_t* red = reinterpret_cast<f32x4_t*>(smem);  // [wave][MB][64]
+  f32x4_t* red = reinterpret_cast<f32x4_t*>(smem);  // [wave][2][MB][64]
 #pragma unroll
-  for (int b = 0; b < MB; b++) red[(wave * MB + b) * 64 + lane] = acc[b];
+  for (int r = 0; r < 2; r++)
+#pragma unroll
+    for (int b = 0; b < MB; b++) red[((wave * 2 + r) * MB + b) * 64 + lane] = acc[r][b];
   lds_barrier();
-  // output block (row tile t, row block b) = group 0 + group 1 (waves t, t + 4)
+  // output block (row tile t, row block b): the four group waves of pair
+  // t / 2 (waves 4 (t / 2) + g), summed in order g = 0..3
   for (int ob = wave; ob < 4 * MB; ob += 8) {
     const int t = ob / MB, b = ob % MB;
-    f32x4_t v = red[(t * MB + b) * 64 + lane];
-    const f32x4_t o = red[((t + 4) * MB + b) * 64 + lane];
-    v[0] += o[0];
-    v[1] += o[1];
-    v[2] += o[2];
-    v[3] += o[3];
+    f32x4_t v = red[(((4 * (t >> 1)) * 2 + (t & 1)) * MB + b) * 64 + lane];
+#pragma unroll
+    for (int g = 1; g < 4; g++) {
+      const f32x4_t o = red[(((4 * (t >> 1) + g) * 2 + (t & 1)) * MB + b) * 64 + lane];
+      v[0] += o[0];
+      v[1] += o[1];
+      v[2] += o[2];
+      v[3] += o[3];
+    }
     const int n = n0 + 16 * t + ln;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
