@@ -312,62 +312,62 @@ __global__ void __launch_bounds__(512) qmv_kernel(const uint16_t* __restrict__ x
 // K tile per pipeline step.  Its operands reach LDS through direct-to-LDS
 // buffer loads (buffer_load_dwordx4 ... lds: each lane's 16 bytes land at
 // base + 16 lane), so nothing in flight occupies registers and the rings can
-// be deep:
-//   * weight ring, NSW slots: the tile's 4 x 1 KB of codes (16 rows x 64
-//     bytes per load: piece q of row n at (16 q + n) 16 bytes, so k-step q's
-//     MFMA operand is one 4-byte LDS read per lane); the codes go out WB = 4
-//     tiles at a time, each with the 64 rows' scales and biases of its 4
-//     tiles (16 bytes a row: a 4-byte load per row and tile would touch 64
-//     lines for 256 bytes);
-//   * x ring, NSX slots: the MB x 4 A operand blocks (1 KB each, lane l =
-//     row l % 16, x values 8 (l / 16) .. + 8 of the k-step, natural order).
+// be deep.  Every load reads 4 rows x 256 contiguous bytes (whole 128-byte
+// lines; 16 rows x 64 bytes a load ran the x stream from L2 at a third of
+// the rate), its 16-byte pieces XOR-swizzled by row in LDS so that an MFMA
+// operand read (16 rows, one piece each) touches every bank once:
+//   * weight ring, NSB slots of WB = 4 K tiles (a batch: 64 rows x 256
+//     bytes of codes, plus the 64 rows' scales and biases of the 4 tiles,
+//     16 bytes a row -- a 4-byte load per row and tile would touch 64 lines
+//     for 256 bytes); a code operand (k-step j of tile t, 8 codes of a row)
+//     is one 4-byte LDS read per lane;
+//   * x ring, NSX slots of one K tile: MB row blocks x 16 rows x 256 bytes;
+//     an A operand (8 x values of a row, natural order) is one 16-byte read.
 // Waves 0..3 issue the weight loads (row tile w; wave 0 also the scales,
 // wave 1 the biases), waves 4..7 the x loads (k-step w - 4 of every row
 // block): a wave waits only for its own loads (vector memory counts complete
 // in order per wave), so the x stream, which comes from L2, never waits
 // behind the weight stream from HBM.  Per step every wave waits for its
 // loads of the step, one barrier publishes the step and frees the slots of
-// the one before, and the next loads go out (x: the step NSX - 1 ahead;
-// weights, at a batch's first step: the batch NSB - 1 ahead).
-// Every wave computes: wave w takes row tile w % 4 and group w / 4 of the K
-// tile (two k-steps) for all MB row blocks: X = x against ones and D = x
-// against the exact codes (natural slot order: (128 or 1024) + c), folded as
-// acc += s D + (b - OFF s) X.  The two group halves are summed in LDS in
-// fixed order; K splits (blockIdx.z = batch * KS + split) write fp32
-// partials for qmm_splitk_reduce_kernel.  Rows past M or N read zeros (the
-// descriptors end there) and are not stored; steps past the split's end load
-// nothing (offsets past the descriptors), so every wave issues the same
-// count each step and its wait counts stay exact.
+// the ones before, and the next loads go out (x: the steps NSX - 2 and
+// NSX - 1 ahead; weights, at a batch's first pair: the batch NSB - 1 ahead).
+// Every wave computes, two steps at a time: wave w takes group w % 4 of the
+// pair (two k-steps) for row tiles 2 (w / 4), 2 (w / 4) + 1 and all MB row
+// blocks: X = x against ones and D = x against the exact codes (natural slot
+// order: (128 or 1024) + c), folded as acc += s D + (b - OFF s) X.  The four
+// group partials of a row tile are summed in LDS in fixed order; K splits
+// (blockIdx.z = batch * KS + split) write fp32 partials for
+// qmm_splitk_reduce_kernel.  Rows past M or N read zeros (the descriptors
+// end there) and are not stored; steps past the split's end load nothing
+// (offsets past the descriptors), so every wave issues the same count each
+// step and its wait counts stay exact.
 template <int MB>
 struct DmaShape {
-  static constexpr int WB = 4;                                  // K tiles per weight batch
-  static constexpr int NSW = MB >= 3 ? 12 : MB == 2 ? 16 : 20;  // weight ring slots (K tiles)
-  static constexpr int NSB = NSW / WB;                          // scale ring slots (batches)
-  static constexpr int NSX = MB == 4 ? 6 : 8;                   // x ring slots (K tiles)
-  static constexpr int WSLOT = 4 * 1024;                        // codes of a K tile
-  static constexpr int SSLOT = 2 * 1024;                        // scales, biases of a batch
-  static constexpr int XSLOT = MB * 4 * 1024;                   // x operand blocks of a K tile
-  static constexpr int SOFF = NSW * WSLOT;
+  static constexpr int WB = 4;                   // K tiles per weight batch (256 bytes of a row)
+  static constexpr int NSB = MB >= 3 ? 3 : MB == 2 ? 4 : 5;  // weight ring slots (batches)
+  static constexpr int NSX = MB == 4 ? 6 : 8;    // x ring slots (K tiles)
+  static constexpr int WSLOT = 16 * 1024;        // codes of a batch: 64 rows x 256 bytes
+  static constexpr int SSLOT = 2 * 1024;         // scales, biases of a batch
+  static constexpr int XSLOT = MB * 4 * 1024;    // x of a K tile: MB row blocks x 16 rows x 256 bytes
+  static constexpr int SOFF = NSB * WSLOT;
   static constexpr int XOFF = SOFF + NSB * SSLOT;
   static constexpr int LDS = XOFF + NSX * XSLOT;
   // The loop runs steps in pairs (c, c + 1), c even; a weight batch is two
-  // pairs.  Loads a weight wave issues per batch: (waves 0, 1) the batch's
-  // scales or biases, then its row tile's codes of the WB tiles.  Before the
-  // pair it waits for step c + 1's codes (which covers step c and the
-  // batch's scales, issued before them): at a batch's first pair, batches up
-  // to k + NSB - 2 are out and 2 codes of batch k follow step c + 1's; at its
-  // second pair batch k + NSB - 1 is out too and none of batch k follow.
+  // pairs.  A weight wave issues LB loads per batch: (waves 0, 1) the
+  // batch's scales or biases, then its row tile's codes (4 loads of 4 rows x
+  // the batch's 256 bytes, so every step needs all of them).  At a batch's
+  // first pair it waits for the whole batch: batches up to k + NSB - 2 are
+  // out then, NSB - 2 of them after batch k.
   template <int LB>
-  static constexpr int wait_w(bool second) {
-    return second ? (NSB - 1) * LB : 2 + (NSB - 2) * LB;
+  static constexpr int wait_w() {
+    return (NSB - 2) * LB;
   }
   // x waves: steps up to c + NSX - 3 are out before the pair (two a pair,
   // NSX - 2 in the prologue), NSX - 4 steps follow step c + 1's
   static constexpr int WAIT_X = (NSX - 4) * MB;
   static constexpr int RED = 8 * 2 * MB * 64 * 16;  // per-wave accumulators at the end
   static_assert(LDS <= 160 * 1024 && RED <= LDS, "LDS budget");
-  static_assert(NSW % WB == 0 && WB == 4 && NSB >= 2 && NSX % 2 == 0 && NSX >= 4 && wait_w<5>(true) <= 63 &&
-                    WAIT_X <= 63,
+  static_assert(WB == 4 && NSB >= 2 && NSX % 2 == 0 && NSX >= 4 && wait_w<5>() <= 63 && WAIT_X <= 63,
                 "ring / vmcnt range");
 };
 
@@ -413,7 +413,7 @@ __global__ void __launch_bounds__(512) qmm_dma_kernel(const uint16_t* __restrict
                                                       const uint16_t* __restrict__ biases, int N, BatchMap bm, int KS,
                                                       int KTS, uint16_t* __restrict__ y, float* __restrict__ part) {
   using SH = DmaShape<MB>;
-  constexpr int NSW = SH::NSW, NSX = SH::NSX;
+  constexpr int NSX = SH::NSX;
   constexpr float OFF = Mma<T>::MAGIC_VAL;
   constexpr uint32_t OOB = 0x80000000u;
   extern __shared__ __align__(16) uint8_t smem[];
@@ -452,45 +452,55 @@ __global__ void __launch_bounds__(512) qmm_dma_kernel(const uint16_t* __restrict
   // the batch's 16-byte scale / bias load covers tiles sload(k) .. + 3 of
   // every row: the batch's own, shifted back to stay inside the row
   auto sload = [&](int k) { return min(tile0(k), KT - WB); };
-  // waves 0..3: codes of row tile `wave` (lane: row ln, piece lq)
-  const uint32_t voff_w = (uint32_t)(16 * wave + ln) * row_bytes + 16u * lq;
+  // Loads write each lane's 16 bytes at base + 16 lane, 4 rows x 256 bytes a
+  // load (16 lanes a row: whole 128-byte lines; 16 rows x 64 bytes a load
+  // reads x from L2 at a third of the rate).  Lane l of a load takes row
+  // 4 i + l / 16 of its 16-row block and 16-byte piece (l % 16) ^ (row % 16)
+  // of the 256 bytes, so piece P of block row r sits in slot
+  // (r / 4) * 64 + (r % 4) * 16 + (P ^ r) (16-byte units): an MFMA operand
+  // read (16 rows, one piece each) spreads over all LDS banks.
+  auto lane_off = [&](int i, uint32_t pitch) {  // load i of a 16-row block: row 4 i + l / 16
+    const int r = 4 * i + (lane >> 4);
+    return (uint32_t)r * pitch + (uint32_t)((lane & 15) ^ r) * 16u;
+  };
+  // waves 0..3: codes of row tile `wave` (loads i < 4)
+  uint32_t voff_w[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) voff_w[i] = (uint32_t)(16 * wave) * row_bytes + lane_off(i, row_bytes);
   // waves 0, 1: scales / biases (lane: row `lane`, 4 tiles' 8 groups)
   const uint32_t voff_sb = (uint32_t)lane * (uint32_t)G * 2u;
-  // waves 4..7: k-step wave - 4 of row block b (lane: row 16 b + ln, values 8 lq ..)
-  const uint32_t voff_x = (uint32_t)ln * (uint32_t)K * 2u + (uint32_t)(32 * (wave - 4) + 8 * lq) * 2u;
+  // waves 4..7: load wave - 4 of every row block
+  const uint32_t voff_x = lane_off(wave & 3, (uint32_t)K * 2u);
   auto issue_w = [&](int k) {  // batch k, weight waves: scales / biases first, then the codes
     const int t0 = tile0(k);
+    const bool live = WB * k < nch;
     if (wave < 2)
       dma_load16(wave == 0 ? rs : rb, smem + SH::SOFF + (k % NSB) * SH::SSLOT + wave * 1024,
-                 WB * k < nch ? voff_sb + (uint32_t)sload(k) * 4u : OOB);
+                 live ? voff_sb + (uint32_t)sload(k) * 4u : OOB);
+    // past the split's end (a partial batch) the loads read on into the row,
+    // or read 0 past the matrix: those tiles are never computed
 #pragma unroll
-    for (int p = 0; p < WB; p++) {
-      const int c = WB * k + p;
-      dma_load16(rw, smem + (c % NSW) * SH::WSLOT + wave * 1024,
-                 c < nch ? voff_w + (uint32_t)(t0 + p) * 64u : OOB);
-    }
+    for (int i = 0; i < 4; i++)
+      dma_load16(rw, smem + (k % NSB) * SH::WSLOT + wave * 4096 + i * 1024,
+                 live ? voff_w[i] + (uint32_t)t0 * 64u : OOB);
   };
   auto issue_x = [&](int c) {  // step c, x waves
     const int kt = tile0(c / WB) + c % WB;
-    uint8_t* slot = xring + (c % NSX) * SH::XSLOT;
+    uint8_t* slot = xring + (c % NSX) * SH::XSLOT + (wave - 4) * 1024;
 #pragma unroll
     for (int b = 0; b < MB; b++)
-      dma_load16(rx, slot + (b * 4 + (wave - 4)) * 1024,
+      dma_load16(rx, slot + b * 4096,
                  c < nch ? voff_x + (uint32_t)(16 * b) * (uint32_t)K * 2u + (uint32_t)kt * 256u : OOB);
   };
-  auto wait_w = [&](bool second) {
-    if (wave < 2) {
-      if (second)
-        wait_vmcnt<SH::template wait_w<WB + 1>(true)>();
-      else
-        wait_vmcnt<SH::template wait_w<WB + 1>(false)>();
-    } else {
-      if (second)
-        wait_vmcnt<SH::template wait_w<WB>(true)>();
-      else
-        wait_vmcnt<SH::template wait_w<WB>(false)>();
-    }
+  auto wait_w = [&]() {
+    if (wave < 2)
+      wait_vmcnt<SH::template wait_w<5>()>();
+    else
+      wait_vmcnt<SH::template wait_w<4>()>();
   };
+  // 16-byte unit of piece P of row r of a 16-row block
+  auto slot16 = [](int r, int P) { return (r >> 2) * 64 + (r & 3) * 16 + (P ^ r); };
+
   // compute: of each pair of steps, wave w takes group gi = w % 4 (step
   // c + gi / 2, group gi % 2 of its tile) for row tiles 2 h, 2 h + 1
   // (h = w / 4) and every row block: each x operand read serves two row
@@ -510,10 +520,10 @@ __global__ void __launch_bounds__(512) qmm_dma_kernel(const uint16_t* __restrict
   for (int c = 0; c < nch; c += 2) {
     const int k = c / WB;
     const bool second = (c % WB) != 0;
-    if (wave < 4)
-      wait_w(second);
-    else
+    if (wave >= 4)
       wait_vmcnt<SH::WAIT_X>();
+    else if (!second)
+      wait_w();
     dma_barrier();  // steps c, c + 1 in LDS everywhere; the slots of the steps before free
     if (wave >= 4) {
       issue_x(c + NSX - 2);
@@ -523,8 +533,9 @@ __global__ void __launch_bounds__(512) qmm_dma_kernel(const uint16_t* __restrict
     }
     const int st = c + (gi >> 1), kg = gi & 1;
     if (st >= nch) continue;  // the odd last step (wave-uniform)
-    const uint8_t* ws = smem + (st % NSW) * SH::WSLOT;
+    const uint8_t* ws = smem + (k % NSB) * SH::WSLOT;
     const uint8_t* xs = xring + (st % NSX) * SH::XSLOT;
+    const int tb = st % WB;  // the step's tile in the batch
     // (s, b) of group 2 kt + kg of row 16 rt + ln: halfword 2 (kt - sload) + kg
     // of the row's 16 bytes
     float sc[2], bp[2];
@@ -549,10 +560,10 @@ __global__ void __launch_bounds__(512) qmm_dma_kernel(const uint16_t* __restrict
 #pragma unroll
       for (int r = 0; r < 2; r++)
         bop[r] = nat_operand<T>(
-            *reinterpret_cast<const uint32_t*>(ws + (2 * h + r) * 1024 + (16 * j + ln) * 16 + 4 * lq));
+            *reinterpret_cast<const uint32_t*>(ws + (2 * h + r) * 4096 + slot16(ln, 4 * tb + j) * 16 + 4 * lq));
 #pragma unroll
       for (int b = 0; b < MB; b++) {
-        const u32x4_t a = *reinterpret_cast<const u32x4_t*>(xs + (b * 4 + j) * 1024 + lane * 16);
+        const u32x4_t a = *reinterpret_cast<const u32x4_t*>(xs + b * 4096 + slot16(ln, 4 * j + lq) * 16);
         X[b] = Mma<T>::mma(a, ones, X[b]);
         D[0][b] = Mma<T>::mma(a, bop[0], D[0][b]);
         D[1][b] = Mma<T>::mma(a, bop[1], D[1][b]);
