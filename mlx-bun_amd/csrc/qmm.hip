@@ -384,9 +384,10 @@ __device__ __forceinline__ void wait_vmcnt() {
 // for explicitly before it).
 __device__ __forceinline__ void dma_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
-__device__ __forceinline__ void dma_load16(__amdgpu_buffer_rsrc_t r, const void* lds, uint32_t voff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(uintptr_t)lds, 16, voff, 0, 0,
-                                           0);
+typedef __attribute__((address_space(3))) uint8_t lds_u8;  // LDS byte (32-bit addresses)
+
+__device__ __forceinline__ void dma_load16(__amdgpu_buffer_rsrc_t r, lds_u8* lds, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 16, voff, 0, 0, 0);
 }
 // MFMA B operand from 8 4-bit codes in natural slot order: dword t holds
 // (OFF + c_2t, OFF + c_2t+1), OFF + c being exact in T (bf16 128 + c =
@@ -435,6 +436,7 @@ __global__ void __launch_bounds__(512) qmm_dma_kernel(const uint16_t* __restrict
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(scales + ((int64_t)wb * N + n0) * G, (uint32_t)nrows * (uint32_t)G * 2u);
   const __amdgpu_buffer_rsrc_t rb = make_rsrc(biases + ((int64_t)wb * N + n0) * G, (uint32_t)nrows * (uint32_t)G * 2u);
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + xb * M * K, xok ? (uint32_t)M * (uint32_t)K * 2u : 0u);
+  lds_u8* const lds = (lds_u8*)smem;  // the same memory through 32-bit LDS addresses
   uint8_t* const xring = smem + SH::XOFF;
 
   // Batch k = steps WB k .. WB k + WB - 1 covers K tiles tile0(k) .. + WB - 1
@@ -475,18 +477,18 @@ __global__ void __launch_bounds__(512) qmm_dma_kernel(const uint16_t* __restrict
     const int t0 = tile0(k);
     const bool live = WB * k < nch;
     if (wave < 2)
-      dma_load16(wave == 0 ? rs : rb, smem + SH::SOFF + (k % NSB) * SH::SSLOT + wave * 1024,
+      dma_load16(wave == 0 ? rs : rb, lds + SH::SOFF + (k % NSB) * SH::SSLOT + wave * 1024,
                  live ? voff_sb + (uint32_t)sload(k) * 4u : OOB);
     // past the split's end (a partial batch) the loads read on into the row,
     // or read 0 past the matrix: those tiles are never computed
 #pragma unroll
     for (int i = 0; i < 4; i++)
-      dma_load16(rw, smem + (k % NSB) * SH::WSLOT + wave * 4096 + i * 1024,
+      dma_load16(rw, lds + (k % NSB) * SH::WSLOT + wave * 4096 + i * 1024,
                  live ? voff_w[i] + (uint32_t)t0 * 64u : OOB);
   };
   auto issue_x = [&](int c) {  // step c, x waves
     const int kt = tile0(c / WB) + c % WB;
-    uint8_t* slot = xring + (c % NSX) * SH::XSLOT + (wave - 4) * 1024;
+    lds_u8* slot = lds + SH::XOFF + (c % NSX) * SH::XSLOT + (wave - 4) * 1024;
 #pragma unroll
     for (int b = 0; b < MB; b++)
       dma_load16(rx, slot + b * 4096,
@@ -546,13 +548,9 @@ __global__ void __launch_bounds__(512) qmm_dma_kernel(const uint16_t* __restrict
       sc[r] = Conv<T>::from_bits(*reinterpret_cast<const uint16_t*>(ss));
       bp[r] = Conv<T>::from_bits(*reinterpret_cast<const uint16_t*>(ss + 1024)) - OFF * sc[r];
     }
+    // the group's first k-step starts X and D from an inline 0 (no zeroing moves)
+    const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
     f32x4_t X[MB], D[2][MB];
-#pragma unroll
-    for (int b = 0; b < MB; b++) {
-      X[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      D[0][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      D[1][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    }
 #pragma unroll
     for (int jj = 0; jj < 2; jj++) {
       const int j = 2 * kg + jj;
@@ -564,9 +562,9 @@ __global__ void __launch_bounds__(512) qmm_dma_kernel(const uint16_t* __restrict
 #pragma unroll
       for (int b = 0; b < MB; b++) {
         const u32x4_t a = *reinterpret_cast<const u32x4_t*>(xs + b * 4096 + slot16(ln, 4 * j + lq) * 16);
-        X[b] = Mma<T>::mma(a, ones, X[b]);
-        D[0][b] = Mma<T>::mma(a, bop[0], D[0][b]);
-        D[1][b] = Mma<T>::mma(a, bop[1], D[1][b]);
+        X[b] = Mma<T>::mma(a, ones, jj ? X[b] : zero);
+        D[0][b] = Mma<T>::mma(a, bop[0], jj ? D[0][b] : zero);
+        D[1][b] = Mma<T>::mma(a, bop[1], jj ? D[1][b] : zero);
       }
     }
 #pragma unroll
