@@ -1006,7 +1006,7 @@ __global__ void __launch_bounds__(256) qmm_splitk_reduce_kernel(const float4* __
 // (x staging amortised over 128 weight rows), 128 x 128 once those give every
 // CU a workgroup, else 64 x 64; K is split (fp32 partials + reduce) until every CU
 // has a workgroup, keeping at least 8 K-steps per split.
-// MLXQ_QMM_KS: fixed K split (power of two) for the tiled GEMM (tuning)
+// MLXQ_QMM_KS: fixed K split (power of two) for the tiled and direct-to-LDS GEMMs (tuning)
 int qmm_ks_override() {
   static const int v = [] {
     const char* e = getenv("MLXQ_QMM_KS");
