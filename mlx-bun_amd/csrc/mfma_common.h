@@ -102,6 +102,17 @@ __device__ __forceinline__ uint32_t buf_load16(__amdgpu_buffer_rsrc_t r, uint32_
   return __builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, (int)soff, AUX);
 }
 
+// s_waitcnt vmcnt(N) alone (expcnt and lgkmcnt left at their maxima): the
+// kernels that load straight into LDS wait on their own counts (the compiler
+// does not track those loads' data)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N <= 63, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+typedef __attribute__((address_space(3))) uint8_t lds_u8;  // LDS byte (32-bit addresses)
+
 // Workgroup barrier that orders LDS only.  __syncthreads() also orders
 // global memory, which compiles to s_waitcnt vmcnt(0) before s_barrier: every
 // wave would wait for all of its outstanding global loads, draining any

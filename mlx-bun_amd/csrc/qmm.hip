@@ -371,20 +371,11 @@ struct DmaShape {
                 "ring / vmcnt range");
 };
 
-// s_waitcnt vmcnt(N) alone (expcnt and lgkmcnt left at their maxima)
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N <= 63, "vmcnt");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
 // s_barrier that also keeps the compiler from moving memory accesses across
 // it.  Unlike a release fence on LDS it does not make the compiler wait for
 // the direct-to-LDS loads in flight (those are tracked by vmcnt and waited
 // for explicitly before it).
 __device__ __forceinline__ void dma_barrier() { asm volatile("s_barrier" ::: "memory"); }
-
-typedef __attribute__((address_space(3))) uint8_t lds_u8;  // LDS byte (32-bit addresses)
 
 __device__ __forceinline__ void dma_load16(__amdgpu_buffer_rsrc_t r, lds_u8* lds, uint32_t voff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 16, voff, 0, 0, 0);
