@@ -256,13 +256,17 @@ def test_gather_qmm_sorted_rows_and_bad_index(O, mlxq_dev, experts_up):
     assert_close(got[:7], ref, what="sorted", dtype=BF16)
 
 
-def test_gather_qmm_many_rows_per_expert(O, mlxq_dev, experts_up):
-    """M = 40 rows per gathered matmul (the tiled GEMM through the batch map)."""
+@pytest.mark.parametrize("path", ["dma", "tile"])
+def test_gather_qmm_many_rows_per_expert(O, mlxq_dev, experts_up, monkeypatch, path):
+    """M = 40 rows per gathered matmul through the batch map: the
+    direct-to-LDS kernel, and (MLXQ_QMM_STREAM=0) the tiled GEMM."""
+    if path == "tile":
+        monkeypatch.setenv("MLXQ_QMM_STREAM", "0")
     idx = np.array([5, 2], np.uint32)
     x = rng_t(O, (2, 40, 2816), 51, BF16)
     got = _gather(O, x, experts_up, idx, 64, 4, BF16)
     ref = _gather_ref(O, x, experts_up, idx, [0, 1], 64, 4, BF16)
-    assert_close(got, ref, what="tile gather", dtype=BF16)
+    assert_close(got, ref, what=f"{path} gather", dtype=BF16)
 
 
 # ------------------------------------------------- gather_qmm, sorted rows
