@@ -63,6 +63,24 @@ def test_qmv_qmm_down_proj(O, mlxq_dev, w_down, M):
     assert_close(y, x.astype(np.float64) @ wd.T, what=f"down M={M}", dtype=BF16)
 
 
+@pytest.mark.parametrize("dtype,N,K", [
+    (BF16, 1000, 2048),   # ragged N
+    (F16, 333, 2816),     # 22 tiles (the tied-head and MoE gate_up K)
+    (BF16, 77, 14336),    # 112 tiles
+    (F16, 4097, 6144),    # one row past a workgroup multiple
+    (BF16, 9, 3072),      # fewer rows than one row tile
+    (F16, 50, 1280),      # 10 tiles
+])
+def test_qmv_one_row_shapes(O, mlxq_dev, dtype, N, K):
+    """One activation row (qmv, 4-bit, group 64) against the float64
+    reference: K from 10 to 112 tiles, ragged N, fewer rows than a workgroup."""
+    w = rng_t(O, (N, K), 13, dtype, 0.05)
+    wq = O.quantize(w, 64, 4, dtype)
+    x = rng_t(O, (1, K), 14, dtype)
+    y = run_qmm(O, mlxq_dev, x, wq, 64, 4, dtype)
+    assert_close(y, x.astype(np.float64) @ deq64(O, *wq, 64, 4, dtype).T, what="dot", dtype=dtype)
+
+
 @pytest.mark.parametrize("dtype,bits,gs,M,N,K", [
     (F16, 4, 64, 3, 200, 512),
     (F16, 8, 64, 5, 130, 768),
@@ -232,7 +250,7 @@ def experts_up(O):
     return O.quantize(w, 64, 4, BF16)
 
 
-@pytest.mark.parametrize("B", [1, 4])
+@pytest.mark.parametrize("B", [1, 4, 8])
 def test_gather_qmm_moe_decode(O, mlxq_dev, experts_up, B):
     """SwitchGLU decode: x [B, 1, H] -> [B, 1, 1, 1, H] against top-8 indices
     [B, 1, 8] (qmv per (token, expert) through the row map)."""
