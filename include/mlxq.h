@@ -230,6 +230,26 @@ int mlxq_quantized_sdpa(const void* q, int dtype, int B, int Hq, int Hkv, int Lq
                         const int32_t* ring_offset, int mask_mode, int window, float scale,
                         int group_size, int bits, void* out, void* stream);
 
+/* quantizedSdpa under an "array" mask that is neither the causal matrix nor a
+ * causal sliding window -- replaces the where(mask, scores, FINFO_MIN) of the
+ * unfused path, src/model/gemma4-base.ts:1320-1327, where the dispatch sends
+ * every such mask (:1543-1545, :1577).  mask: device uint8, nonzero = attend:
+ * query i of row b attends logical key j (0 <= j < valid, slot(j) as above)
+ * iff mask[b * mask_batch_stride + i * mask_row_stride + j] != 0; a batch
+ * stride of 0 shares one [Lq, .] mask across the batch, and mask_row_stride
+ * must be >= n_kv (>= kv_capacity with valid_len).  A query with no attended
+ * key averages V over its valid keys, as the reference's softmax over
+ * all-FINFO_MIN scores does.  Other arguments and rounding as
+ * mlxq_quantized_sdpa (no mask_mode / window); runs the generic VALU kernel,
+ * no device allocation. */
+int mlxq_quantized_sdpa_array_mask(const void* q, int dtype, int B, int Hq, int Hkv, int Lq, int D,
+                                   const uint32_t* k_packed, const void* k_scales, const void* k_biases,
+                                   const uint32_t* v_packed, const void* v_scales, const void* v_biases,
+                                   int64_t kv_capacity, int64_t n_kv, const int32_t* valid_len,
+                                   const int32_t* ring_offset, const uint8_t* mask, int64_t mask_batch_stride,
+                                   int64_t mask_row_stride, float scale, int group_size, int bits, void* out,
+                                   void* stream);
+
 /* mlxq_quantized_sdpa without any device allocation.  No counterpart in the
  * reference: it is for callers that cannot allocate device memory -- code
  * under HIP graph capture, tight serving loops, harnesses that forbid

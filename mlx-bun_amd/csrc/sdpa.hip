@@ -1884,12 +1884,18 @@ int launch_prefill(int D, int gs, const void* q, int B, int Hq, int Hkv, int Lq,
 // One workgroup (128 threads) per (batch row, q head, query).  Scores for
 // 128 keys at a time (one key per thread, fp32 dot of fp32-dequantized K),
 // online softmax through LDS, values accumulated with threads over d.
+// With an array mask (amask != null; causal = window = 0) key j of query i
+// of row b is attended iff amask[b mask_bs + i mask_rs + j] != 0, and a
+// query with no attended key averages V over all its valid keys: the
+// reference's where(mask, scores, FINFO_MIN) followed by a softmax gives
+// every key the same weight when all of them are masked.
 template <typename T, int BITS>
 __global__ void __launch_bounds__(128) sdpa_generic_kernel(
     const void* __restrict__ qv, const uint32_t* __restrict__ kp, const void* __restrict__ ksv,
     const void* __restrict__ kbv, const uint32_t* __restrict__ vp, const void* __restrict__ vsv,
     const void* __restrict__ vbv, int Hq, int Hkv, int Lq, int D, int gs, Geometry geo, int causal, int window,
-    float scale, void* __restrict__ outv) {
+    float scale, void* __restrict__ outv, const uint8_t* __restrict__ amask = nullptr, int64_t mask_bs = 0,
+    int64_t mask_rs = 0) {
   using S = typename T::storage;
   const S* q = reinterpret_cast<const S*>(qv);
   const S* ks = reinterpret_cast<const S*>(ksv);
@@ -1928,10 +1934,30 @@ __global__ void __launch_bounds__(128) sdpa_generic_kernel(
   for (int k = 0; k < MAXD / 128; k++) o[k] = 0.f;
   __syncthreads();
 
+  const uint8_t* mrow = amask ? amask + (int64_t)b * mask_bs + (int64_t)i * mask_rs : nullptr;
+  // o = sum over the keys c0 .. c0 + nkeys - 1 of sc[key] V[key], o scaled by alpha first
+  auto accumulate_v = [&](int64_t c0, int nkeys, float alpha) {
+#pragma unroll
+    for (int k = 0; k < MAXD / 128; k++) {
+      const int d = tid + 128 * k;
+      if (d < D) {
+        float acc = o[k] * alpha;
+        for (int jj = 0; jj < nkeys; jj++) {
+          const int64_t row = rowbase + slot_of(base_slot, c0 + jj, geo.cap);
+          const float cv = (float)((vp[row * KW + d / E] >> (BITS * (d % E))) & MASK);
+          const float wv = Conv<T>::load(vs, row * G + d / gs) * cv + Conv<T>::load(vb, row * G + d / gs);
+          acc += sc[jj] * wv;
+        }
+        o[k] = acc;
+      }
+    }
+  };
+
   for (int64_t c0 = jbeg; c0 < jend; c0 += 128) {
     const int64_t j = c0 + tid;
+    const bool attend = j < jend && (!mrow || mrow[j] != 0);
     float s = -INFINITY;
-    if (j < jend) {
+    if (attend) {
       const int64_t row = rowbase + slot_of(base_slot, j, geo.cap);
       const uint32_t* kr = kp + row * KW;
       float acc = 0.f;
@@ -1951,8 +1977,9 @@ __global__ void __launch_bounds__(128) sdpa_generic_kernel(
       __syncthreads();
     }
     const float m_new = fmaxf(m_run, red[0]);
-    const float alpha = exp2f(m_run - m_new);
-    const float pj = j < jend ? exp2f(s - m_new) : 0.f;
+    // (a chunk with no attended key leaves m at -inf: nothing to rescale)
+    const float alpha = m_new == -INFINITY ? 1.0f : exp2f(m_run - m_new);
+    const float pj = attend ? exp2f(s - m_new) : 0.f;
     sc[tid] = pj;
     __syncthreads();
     red[tid] = pj;
@@ -1963,22 +1990,17 @@ __global__ void __launch_bounds__(128) sdpa_generic_kernel(
     }
     l_run = l_run * alpha + red[0];
     m_run = m_new;
-    const int nkeys = (int)min((int64_t)128, jend - c0);
-#pragma unroll
-    for (int k = 0; k < MAXD / 128; k++) {
-      const int d = tid + 128 * k;
-      if (d < D) {
-        float acc = o[k] * alpha;
-        for (int jj = 0; jj < nkeys; jj++) {
-          const int64_t row = rowbase + slot_of(base_slot, c0 + jj, geo.cap);
-          const float cv = (float)((vp[row * KW + d / E] >> (BITS * (d % E))) & MASK);
-          const float wv = Conv<T>::load(vs, row * G + d / gs) * cv + Conv<T>::load(vb, row * G + d / gs);
-          acc += sc[jj] * wv;
-        }
-        o[k] = acc;
-      }
-    }
+    accumulate_v(c0, (int)min((int64_t)128, jend - c0), alpha);
     __syncthreads();
+  }
+  if (mrow && l_run == 0.f) {  // every valid key masked (workgroup-uniform): the mean of V
+    for (int64_t c0 = 0; c0 < valid; c0 += 128) {
+      sc[tid] = 1.0f;
+      __syncthreads();
+      accumulate_v(c0, (int)min((int64_t)128, valid - c0), 1.0f);
+      __syncthreads();
+    }
+    l_run = (float)valid;
   }
 #pragma unroll
   for (int k = 0; k < MAXD / 128; k++) {
@@ -2140,11 +2162,42 @@ bool decode_mfma_ok(int dtype, int bits, int D, int gs, int nrep, std::initializ
 
 // The whole dispatch of mlxq_quantized_sdpa, with its scratch (split-K
 // partials) taken from `scr`.
-int sdpa_dispatch(const void* q, int dtype, int B, int Hq, int Hkv, int Lq, int D, const uint32_t* k_packed,
-                  const void* k_scales, const void* k_biases, const uint32_t* v_packed, const void* v_scales,
-                  const void* v_biases, int64_t kv_capacity, int64_t n_kv, const int32_t* valid_len,
-                  const int32_t* ring_offset, int mask_mode, int window, float scale, int group_size, int bits,
-                  void* out, void* stream, const mlxq::Scratch& scr) {
+// the generic kernel (every geometry, mask and dtype), with an optional
+// array mask
+int launch_generic(const void* q, int dtype, int B, int Hq, int Hkv, int Lq, int D, const uint32_t* k_packed,
+                   const void* k_scales, const void* k_biases, const uint32_t* v_packed, const void* v_scales,
+                   const void* v_biases, Geometry geo, int causal, int window, float scale, int group_size, int bits,
+                   void* out, hipStream_t s, const uint8_t* amask, int64_t mask_bs, int64_t mask_rs) {
+  dim3 grid((unsigned)Lq, (unsigned)Hq, (unsigned)B);
+  MLXQ_DISPATCH_T(dtype, TT, {
+    switch (bits) {
+      case 2:
+        hipLaunchKernelGGL((sdpa_generic_kernel<TT, 2>), grid, dim3(128), 0, s, q, k_packed, k_scales, k_biases,
+                           v_packed, v_scales, v_biases, Hq, Hkv, Lq, D, group_size, geo, causal, window, scale, out,
+                           amask, mask_bs, mask_rs);
+        break;
+      case 4:
+        hipLaunchKernelGGL((sdpa_generic_kernel<TT, 4>), grid, dim3(128), 0, s, q, k_packed, k_scales, k_biases,
+                           v_packed, v_scales, v_biases, Hq, Hkv, Lq, D, group_size, geo, causal, window, scale, out,
+                           amask, mask_bs, mask_rs);
+        break;
+      default:
+        hipLaunchKernelGGL((sdpa_generic_kernel<TT, 8>), grid, dim3(128), 0, s, q, k_packed, k_scales, k_biases,
+                           v_packed, v_scales, v_biases, Hq, Hkv, Lq, D, group_size, geo, causal, window, scale, out,
+                           amask, mask_bs, mask_rs);
+        break;
+    }
+  });
+  MLXQ_LAUNCHED("sdpa_generic_kernel");
+  return MLXQ_OK;
+}
+
+// argument checks shared by the entry points (buffers only when there is
+// work: an empty batch, head or query extent is a no-op)
+int check_sdpa_args(const void* q, int dtype, int B, int Hq, int Hkv, int Lq, int D, const uint32_t* k_packed,
+                    const void* k_scales, const void* k_biases, const uint32_t* v_packed, const void* v_scales,
+                    const void* v_biases, int64_t kv_capacity, int64_t n_kv, const int32_t* valid_len,
+                    const int32_t* ring_offset, int group_size, int bits, const void* out) {
   MLXQ_REQUIRE_INIT();
   MLXQ_CHECK(mlxq::dtype_supported(dtype), "dtype must be float16, bfloat16 or float32");
   MLXQ_CHECK(bits == 2 || bits == 4 || bits == 8, "bits must be 2, 4 or 8");
@@ -2155,12 +2208,24 @@ int sdpa_dispatch(const void* q, int dtype, int B, int Hq, int Hkv, int Lq, int 
   MLXQ_CHECK(kv_capacity > 0, "kv_capacity must be positive");
   MLXQ_CHECK(valid_len || (n_kv >= 0 && n_kv <= kv_capacity), "n_kv must lie in [0, kv_capacity]");
   MLXQ_CHECK(!ring_offset || valid_len, "ring_offset requires valid_len");
-  MLXQ_CHECK(mask_mode == MLXQ_MASK_NONE || mask_mode == MLXQ_MASK_CAUSAL, "unknown mask mode");
-  MLXQ_CHECK(window >= 0, "negative window");
   if (B == 0 || Hq == 0 || Lq == 0) return MLXQ_OK;
   MLXQ_CHECK(q && k_packed && k_scales && k_biases && v_packed && v_scales && v_biases && out, "null buffer");
   MLXQ_CHECK((uintptr_t)q % 16 == 0 && (uintptr_t)k_packed % 16 == 0 && (uintptr_t)v_packed % 16 == 0,
              "q and packed caches must be 16-byte aligned");
+  return MLXQ_OK;
+}
+
+int sdpa_dispatch(const void* q, int dtype, int B, int Hq, int Hkv, int Lq, int D, const uint32_t* k_packed,
+                  const void* k_scales, const void* k_biases, const uint32_t* v_packed, const void* v_scales,
+                  const void* v_biases, int64_t kv_capacity, int64_t n_kv, const int32_t* valid_len,
+                  const int32_t* ring_offset, int mask_mode, int window, float scale, int group_size, int bits,
+                  void* out, void* stream, const mlxq::Scratch& scr) {
+  int rc = check_sdpa_args(q, dtype, B, Hq, Hkv, Lq, D, k_packed, k_scales, k_biases, v_packed, v_scales, v_biases,
+                           kv_capacity, n_kv, valid_len, ring_offset, group_size, bits, out);
+  if (rc) return rc;
+  MLXQ_CHECK(mask_mode == MLXQ_MASK_NONE || mask_mode == MLXQ_MASK_CAUSAL, "unknown mask mode");
+  MLXQ_CHECK(window >= 0, "negative window");
+  if (B == 0 || Hq == 0 || Lq == 0) return MLXQ_OK;
   hipStream_t s = mlxq::resolve_stream(stream);
   Geometry geo{kv_capacity, valid_len ? kv_capacity : n_kv, valid_len, ring_offset};
   const int nrep = Hq / Hkv;
@@ -2221,25 +2286,8 @@ int sdpa_dispatch(const void* q, int dtype, int B, int Hq, int Hkv, int Lq, int 
                      : launch_prefill_wide<F16, 8>(D, group_size, q, B, Hq, Hkv, Lq, k_packed, k_scales, k_biases,
                                                    v_packed, v_scales, v_biases, geo, causal, window, scale, out, s, scr);
   }
-  dim3 grid((unsigned)Lq, (unsigned)Hq, (unsigned)B);
-  MLXQ_DISPATCH_T(dtype, TT, {
-    switch (bits) {
-      case 2:
-        hipLaunchKernelGGL((sdpa_generic_kernel<TT, 2>), grid, dim3(128), 0, s, q, k_packed, k_scales, k_biases,
-                           v_packed, v_scales, v_biases, Hq, Hkv, Lq, D, group_size, geo, causal, window, scale, out);
-        break;
-      case 4:
-        hipLaunchKernelGGL((sdpa_generic_kernel<TT, 4>), grid, dim3(128), 0, s, q, k_packed, k_scales, k_biases,
-                           v_packed, v_scales, v_biases, Hq, Hkv, Lq, D, group_size, geo, causal, window, scale, out);
-        break;
-      default:
-        hipLaunchKernelGGL((sdpa_generic_kernel<TT, 8>), grid, dim3(128), 0, s, q, k_packed, k_scales, k_biases,
-                           v_packed, v_scales, v_biases, Hq, Hkv, Lq, D, group_size, geo, causal, window, scale, out);
-        break;
-    }
-  });
-  MLXQ_LAUNCHED("sdpa_generic_kernel");
-  return MLXQ_OK;
+  return launch_generic(q, dtype, B, Hq, Hkv, Lq, D, k_packed, k_scales, k_biases, v_packed, v_scales, v_biases, geo,
+                        causal, window, scale, group_size, bits, out, s, nullptr, 0, 0);
 }
 
 }  // namespace
@@ -2268,4 +2316,25 @@ extern "C" int mlxq_quantized_sdpa_noalloc(const void* q, int dtype, int B, int 
   return sdpa_dispatch(q, dtype, B, Hq, Hkv, Lq, D, k_packed, k_scales, k_biases, v_packed, v_scales, v_biases,
                        kv_capacity, n_kv, valid_len, ring_offset, mask_mode, window, scale, group_size, bits, out,
                        stream, scr);
+}
+
+extern "C" int mlxq_quantized_sdpa_array_mask(const void* q, int dtype, int B, int Hq, int Hkv, int Lq, int D,
+                                              const uint32_t* k_packed, const void* k_scales, const void* k_biases,
+                                              const uint32_t* v_packed, const void* v_scales, const void* v_biases,
+                                              int64_t kv_capacity, int64_t n_kv, const int32_t* valid_len,
+                                              const int32_t* ring_offset, const uint8_t* mask,
+                                              int64_t mask_batch_stride, int64_t mask_row_stride, float scale,
+                                              int group_size, int bits, void* out, void* stream) {
+  const int rc = check_sdpa_args(q, dtype, B, Hq, Hkv, Lq, D, k_packed, k_scales, k_biases, v_packed, v_scales,
+                                 v_biases, kv_capacity, n_kv, valid_len, ring_offset, group_size, bits, out);
+  if (rc) return rc;
+  MLXQ_CHECK(mask_batch_stride >= 0, "negative mask batch stride");
+  // a row's keys are logical positions 0 .. valid - 1 <= n_kv (kv_capacity with valid_len)
+  MLXQ_CHECK(mask_row_stride >= (valid_len ? kv_capacity : n_kv), "mask rows must cover every key");
+  if (B == 0 || Hq == 0 || Lq == 0) return MLXQ_OK;
+  MLXQ_CHECK(mask, "null mask");
+  Geometry geo{kv_capacity, valid_len ? kv_capacity : n_kv, valid_len, ring_offset};
+  return launch_generic(q, dtype, B, Hq, Hkv, Lq, D, k_packed, k_scales, k_biases, v_packed, v_scales, v_biases, geo,
+                        0, 0, scale, group_size, bits, out, mlxq::resolve_stream(stream), mask, mask_batch_stride,
+                        mask_row_stride);
 }

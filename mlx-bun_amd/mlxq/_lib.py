@@ -28,7 +28,7 @@ SYMBOLS = (
     "mlxq_workspace_reserve", "mlxq_workspace_size",
     "mlxq_quantize", "mlxq_kv_append", "mlxq_dequantize", "mlxq_embedding_gather", "mlxq_quantized_matmul",
     "mlxq_gather_qmm", "mlxq_gather_qmm_sorted",
-    "mlxq_quantized_sdpa", "mlxq_quantized_sdpa_noalloc",
+    "mlxq_quantized_sdpa", "mlxq_quantized_sdpa_noalloc", "mlxq_quantized_sdpa_array_mask",
 )
 
 
@@ -75,6 +75,8 @@ def _declare(L: ctypes.CDLL) -> None:
         "mlxq_gather_qmm_sorted": [P, I, I64, I64, P, P, P, P, I64, I64, I, I, P, P],
         "mlxq_quantized_sdpa": [P, I, I, I, I, I, I, P, P, P, P, P, P, I64, I64, P, P, I, I, F, I, I, P, P],
         "mlxq_quantized_sdpa_noalloc": [P, I, I, I, I, I, I, P, P, P, P, P, P, I64, I64, P, P, I, I, F, I, I, P, P],
+        "mlxq_quantized_sdpa_array_mask": [P, I, I, I, I, I, I, P, P, P, P, P, P, I64, I64, P, P, P, I64, I64, F, I,
+                                           I, P, P],
     }
     for name, args in sig.items():
         fn = getattr(L, name)

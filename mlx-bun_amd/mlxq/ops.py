@@ -223,10 +223,12 @@ def createCausalMask(N: int, offset: int, windowSize: Optional[int]) -> Mask:
     return Mask("array", m, causalEquivalent=windowSize is None, window=windowSize)
 
 
-_MASK_NONE, _MASK_CAUSAL = 0, 1
+_MASK_NONE, _MASK_CAUSAL, _MASK_ARRAY = 0, 1, -1
 
 
 def _mask_args(mask: Mask):
+    """(mode, window) for mlxq_quantized_sdpa; _MASK_ARRAY for an array mask
+    that is neither the causal matrix nor a causal window (applied as given)."""
     if mask is None or mask.mode == "":
         return _MASK_NONE, 0
     if mask.mode == "causal":
@@ -236,8 +238,29 @@ def _mask_args(mask: Mask):
             return _MASK_CAUSAL, 0
         if mask.window is not None:
             return _MASK_CAUSAL, int(mask.window)
-        raise ValueError("quantizedSdpa: only causal / sliding-window array masks are supported")
+        return _MASK_ARRAY, 0
     raise ValueError(f"unknown mask mode {mask.mode!r}")
+
+
+def _array_mask(arr, B: int, L: int, n_keys: int):
+    """A bool mask broadcastable to [B, 1, L, keys] (the reference's unfused
+    path broadcasts it over heads: gemma4-base.ts:1320-1327) as a device uint8
+    [Bm, L, N] plus its (batch, row) strides in elements."""
+    if arr is None:
+        raise ValueError("quantizedSdpa: array mask without an array")
+    m = np.asarray(arr)
+    if m.ndim == 4:
+        if m.shape[1] != 1:
+            raise ValueError("quantizedSdpa: array masks may not vary over heads")
+        m = m[:, 0]
+    if m.ndim == 2:
+        m = m[None]
+    if m.ndim != 3 or m.shape[0] not in (1, B) or m.shape[1] != L:
+        raise ValueError(f"quantizedSdpa: mask shape {np.shape(arr)} does not broadcast to [{B}, 1, {L}, N]")
+    if m.shape[2] < n_keys:
+        raise ValueError(f"quantizedSdpa: mask covers {m.shape[2]} keys, the cache view has {n_keys}")
+    dev = DeviceArray.fromNumpy(np.ascontiguousarray(m != 0, dtype=np.uint8), Dtype.uint8)
+    return dev, (m.shape[1] * m.shape[2] if m.shape[0] > 1 else 0), m.shape[2]
 
 
 def _cache_view(t: QuantizedTensor, what: str):
@@ -273,6 +296,14 @@ def quantizedSdpa(q: DeviceArray, kq: QuantizedTensor, vq: QuantizedTensor, scal
     out = DeviceArray.empty(q.shape, q.dtype)
     vl = validLen.ptr if validLen is not None else None
     ro = ringOffset.ptr if ringOffset is not None else None
+    if mode == _MASK_ARRAY:
+        dm, bstride, rstride = _array_mask(mask.arr, B, L, cap_k if validLen is not None else n_k)
+        _lib.call("mlxq_quantized_sdpa_array_mask", q.ptr, q.dtype, B, Hq, Hkv, L, D,
+                  kq.packed.ptr, kq.scales.ptr, kq.biases.ptr, vq.packed.ptr, vq.scales.ptr, vq.biases.ptr,
+                  cap_k, n_k, vl, ro, dm.ptr, bstride, rstride, ctypes.c_float(scale), groupSize, bits, out.ptr,
+                  None)
+        out._deps = [dm]  # the launch (or a captured graph replaying it) reads the mask after this returns
+        return out
     _lib.call("mlxq_quantized_sdpa", q.ptr, q.dtype, B, Hq, Hkv, L, D,
               kq.packed.ptr, kq.scales.ptr, kq.biases.ptr, vq.packed.ptr, vq.scales.ptr, vq.biases.ptr,
               cap_k, n_k, vl, ro, mode, window, ctypes.c_float(scale), groupSize, bits, out.ptr, None)

@@ -214,6 +214,56 @@ def sdpa_tiled_t(q, kq, vq, *, scale, gs, bits, dtype, cap=None, n_kv=None, vali
     return out
 
 
+# most negative finite value of each score dtype (mlx finfo(T).min)
+FINFO_MIN = {BF16: -3.3895313892515355e38, F16: -65504.0, F32: -3.4028234663852886e38}
+
+
+def sdpa_array_mask(q, kq, vq, mask, *, scale, gs, bits, dtype, cap=None, n_kv=None, valid_len=None,
+                    ring_off=None) -> np.ndarray:
+    """quantizedSdpaUnfused under an "array" mask (src/model/gemma4-base.ts:
+    1320-1334: where(mask, scores, FINFO_MIN[T]), softmax over the keys), in
+    float64 -> [B, Hq, Lq, D].  mask: bool, broadcastable to [B, Lq, n] over
+    logical keys j (temporal order); row b's keys are j < valid (valid_len[b]
+    capped at cap, else n_kv), key j at slot (ring_off[b] - valid + j) mod cap
+    on a ring, else slot j.  q is scaled as T(q * T(scale)) unless scale == 1;
+    K and V are dequantized exactly (s * c + b in float64).  A query with every
+    key masked gets equal weights on all of them, as the reference's softmax
+    over all-FINFO_MIN scores does."""
+    q = np.asarray(q, dtype=np.float32)
+    B, Hq, Lq, D = q.shape
+    kp, ks, kb = kq
+    vp, vs, vb = vq
+    Hkv = kp.shape[1]
+    cap = kp.shape[2] if cap is None else cap
+    n_kv = cap if n_kv is None else n_kv
+
+    def deq(p, s_, b_):
+        c = unpack_codes(p, bits).astype(np.float64)
+        return from_t(s_, dtype).astype(np.float64).repeat(gs, -1) * c + \
+            from_t(b_, dtype).astype(np.float64).repeat(gs, -1)
+
+    K, V = deq(kp, ks, kb), deq(vp, vs, vb)  # [B, Hkv, cap, D]
+    qs = q.astype(np.float64) if scale == 1.0 else \
+        round_t(q * round_t(np.float32(scale), dtype), dtype).astype(np.float64)
+    m = np.broadcast_to(np.asarray(mask, dtype=bool).reshape((-1,) + np.shape(mask)[-2:]), (B, Lq, np.shape(mask)[-1]))
+    out = np.zeros((B, Hq, Lq, D), dtype=np.float64)
+    rep = Hq // Hkv
+    for b in range(B):
+        valid = n_kv if valid_len is None else min(int(valid_len[b]), cap)
+        if valid == 0:
+            continue
+        j = np.arange(valid)
+        slots = (int(ring_off[b]) - valid + j) % cap if ring_off is not None else j
+        for h in range(Hq):
+            Kb, Vb = K[b, h // rep, slots], V[b, h // rep, slots]
+            S = qs[b, h] @ Kb.T  # [Lq, valid]
+            S = np.where(m[b, :, :valid], S, FINFO_MIN[dtype])
+            S = S - S.max(-1, keepdims=True)
+            P = np.exp(S)
+            out[b, h] = (P / P.sum(-1, keepdims=True)) @ Vb
+    return out
+
+
 # ----------------------------------------------------------- ring geometry
 
 def ring_slot_mask(valid: int, ring_off: int, cap: int) -> np.ndarray:

@@ -276,3 +276,44 @@ def test_prefill_unscaled_scores(O, mlxq_dev, Hq, Hkv, L, N, D, gs, bits, dtype)
     q, kq, vq = case(O, 1, Hq, Hkv, L, N, D, gs, bits, dtype, 90 + L)
     got = run(O, mlxq_dev, q, kq, vq, dtype, 1.0, gs, bits, mask=ops.createCausalMask(L, N - L, None))
     check(O, got, q, kq, vq, dtype, 1.0, gs, bits, "prefill scale 1", causal=True)
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,L,N,D,gs,bits,dtype,scale,ring", [
+    (2, 4, 2, 5, 300, 128, 64, 4, BF16, 1.0, False),   # per-row masks, GQA 2
+    (1, 8, 2, 1, 77, 64, 32, 8, F16, 0.125, False),     # decode, one mask for the batch
+    (2, 4, 4, 3, 64, 128, 64, 4, BF16, 1.0, True),      # ring rows: keys in temporal order
+])
+def test_array_mask(O, mlxq_dev, B, Hq, Hkv, L, N, D, gs, bits, dtype, scale, ring):
+    """A general "array" mask (neither causal nor a window: the reference's
+    where(mask, scores, FINFO_MIN), gemma4-base.ts:1320-1327) against the
+    float64 oracle, with a query that attends one key and one that attends
+    none (the mean of V over the row's keys)."""
+    from mlxq import ops
+
+    q, kq, vq = case(O, B, Hq, Hkv, L, N, D, gs, bits, dtype, 60 + L)
+    r = np.random.default_rng(61 + L)
+    shape = (B, 1, L, N) if B > 1 else (L, N)
+    m = r.random(shape) < 0.4
+    flat = m.reshape(-1, L, N)
+    flat[0, 0, :] = False
+    flat[0, 0, N // 3] = True
+    if L > 1:
+        flat[-1, L - 1, :] = False
+    geo = {}
+    if ring:
+        geo = dict(valid_len=np.array([N, N - 20], np.int32), ring_off=np.array([17, 50], np.int32))
+    got = run(O, mlxq_dev, q, kq, vq, dtype, scale, gs, bits, mask=ops.Mask("array", m),
+              valid=geo.get("valid_len"), ring=geo.get("ring_off"))
+    ref = O.sdpa_array_mask(q, kq, vq, m, scale=scale, gs=gs, bits=bits, dtype=dtype, **geo)
+    assert_close(got, ref, what="array mask", dtype=dtype)
+
+
+def test_array_mask_shape_errors(O, mlxq_dev):
+    """Masks that do not broadcast to [B, 1, L, keys] are rejected on the host."""
+    from mlxq import ops
+
+    q, kq, vq = case(O, 2, 4, 2, 3, 40, 64, 64, 4, BF16, 70)
+    for bad in (np.ones((2, 40), bool), np.ones((3, 30), bool), np.ones((2, 2, 3, 40), bool)):
+        with pytest.raises(ValueError):
+            run(O, mlxq_dev, q, kq, vq, BF16, 1.0, 64, 4, mask=ops.Mask("array", bad))
+

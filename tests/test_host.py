@@ -35,8 +35,10 @@ def test_mask_mode_mapping():
     assert ops._mask_args(ops.Mask("causal")) == (1, 0)
     assert ops._mask_args(ops.createCausalMask(4, 8, None)) == (1, 0)
     assert ops._mask_args(ops.createCausalMask(4, 8, 6)) == (1, 6)
+    # any other array mask is applied as given (mlxq_quantized_sdpa_array_mask)
+    assert ops._mask_args(ops.Mask("array", np.ones((2, 2), bool))) == (ops._MASK_ARRAY, 0)
     with pytest.raises(ValueError):
-        ops._mask_args(ops.Mask("array", np.ones((2, 2), bool)))
+        ops._mask_args(ops.Mask("bidir"))
 
 
 def test_cache_make_mask_rules():

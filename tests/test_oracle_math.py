@@ -10,7 +10,8 @@ map, off-by-one mask, ring offset sign) fails it:
   - closed forms: one key -> V row, identical keys -> mean of V, linearity,
   - invariants the reference's own tests assert: tiled vs unfused <= 2/128
     (tests/fused-sdpa.test.ts:98-114), fused decode vs unfused < 0.02
-    (tests/fused-decode-kernel.test.ts:30-67), array causal mask == causal.
+    (tests/fused-decode-kernel.test.ts:30-67), array causal mask == causal;
+    the array-mask restatement against the C oracle's causal / window modes.
 """
 import numpy as np
 import pytest
@@ -236,6 +237,45 @@ def test_causal_string_equals_array_window_none(O):
     a = O.sdpa(q, kq, vq, scale=1.0, gs=c["group"], bits=c["bits"], dtype=O.BF16, causal=True)
     ref = numpy_sdpa(O, q, kq, vq, 1.0, c["group"], c["bits"], O.BF16, causal=True)
     np.testing.assert_allclose(a, ref, rtol=1e-9, atol=1e-12)
+
+
+def test_array_mask_oracle_pins(O):
+    """sdpa_array_mask (where(mask, scores, FINFO_MIN), gemma4-base.ts:1320-1334)
+    against the C oracle's own masks and closed forms: the causal matrix ==
+    causal mode, all-true == no mask, a causal window == window mode, a single
+    attended key -> that key's V row, no attended key -> the mean of V (the
+    reference's softmax over all-FINFO_MIN scores), GQA head map and a ring
+    row's temporal key order."""
+    dtype, gs, bits = 12, 64, 4
+    B, Hq, Hkv, L, N, D = 2, 4, 2, 6, 40, 64
+    q, kq, vq = make_case(O, B, Hq, Hkv, L, N, D, gs, bits, dtype, 31)
+    kw = dict(scale=0.5, gs=gs, bits=bits, dtype=dtype)
+    pos = np.arange(N - L, N)[:, None]
+    j = np.arange(N)[None, :]
+    np.testing.assert_allclose(O.sdpa_array_mask(q, kq, vq, j <= pos, **kw), O.sdpa(q, kq, vq, causal=True, **kw),
+                               rtol=1e-9, atol=1e-12)
+    np.testing.assert_allclose(O.sdpa_array_mask(q, kq, vq, np.ones((L, N), bool), **kw), O.sdpa(q, kq, vq, **kw),
+                               rtol=1e-9, atol=1e-12)
+    np.testing.assert_allclose(O.sdpa_array_mask(q, kq, vq, (j <= pos) & (pos < j + 9), **kw),
+                               O.sdpa(q, kq, vq, causal=True, window=9, **kw), rtol=1e-9, atol=1e-12)
+    vd = deq64(O, *vq, gs, bits, dtype)
+    m = np.zeros((B, 1, L, N), bool)
+    m[0, 0, 0, 17] = True       # row 0 query 0: key 17 only
+    m[1, 0, 2, :] = True        # row 1 query 2: every key
+    got = O.sdpa_array_mask(q, kq, vq, m, **kw)
+    for h in range(Hq):
+        np.testing.assert_allclose(got[0, h, 0], vd[0, h // 2, 17], rtol=1e-12)
+        np.testing.assert_allclose(got[0, h, 1], vd[0, h // 2].mean(0), rtol=1e-10)  # nothing attended
+    np.testing.assert_allclose(got[1, :, 2], O.sdpa(q, kq, vq, **kw)[1, :, 2], rtol=1e-9, atol=1e-12)
+    # a ring row: logical key j sits at slot (ring - valid + j) mod cap
+    ring, valid = np.array([13, 40], np.int32), np.array([40, 25], np.int32)
+    mr = np.random.default_rng(5).random((B, L, N)) < 0.6
+    got = O.sdpa_array_mask(q, kq, vq, mr, valid_len=valid, ring_off=ring, **kw)
+    for b in range(B):
+        slots = (ring[b] - valid[b] + np.arange(valid[b])) % N
+        lin = O.sdpa_array_mask(q[b:b + 1], tuple(t[b:b + 1, :, slots] for t in kq),
+                                tuple(t[b:b + 1, :, slots] for t in vq), mr[b:b + 1, :, :valid[b]], **kw)
+        np.testing.assert_allclose(got[b:b + 1], lin, rtol=1e-12)
 
 
 @pytest.mark.parametrize("site", [  # tests/fused-decode-kernel.test.ts:30-67
