@@ -894,47 +894,62 @@ __global__ void __launch_bounds__(256) qmm_tile_kernel(const uint16_t* __restric
 }
 
 // Work list of mx.gather_qmm over sorted rows: rows with equal consecutive
-// indices form one expert's run, cut into blocks of at most BM (<= 128)
-// rows; item j = (first row, rows, expert) at seg[1 + 3j], the count at
-// seg[0] (at most R items).  One workgroup stages up to 16384 indices (and
-// BM after them) in LDS with every load in flight at once, then walks them
-// 1024 rows at a time: a max-scan of run
-// starts gives each row's run start, a sum-scan numbers the block starts
-// (lane shuffles within a wave, then the 16 wave totals).  Unsorted indices
-// only give shorter runs (every row still lands in one item).
+// indices form one expert's run, cut into blocks of at most BM rows; item j
+// = (first row, rows, expert) at seg[1 + 3j], the count at seg[0] (at most R
+// items).  One workgroup takes the rows 4096 at a time, 4 consecutive rows a
+// thread, all of a pass's index loads in flight at once: a max-scan of run
+// starts gives each row its run's start, a sum-scan numbers the block starts
+// (within the thread, then lane shuffles, then the 16 wave totals).  The
+// pass's item starts stay in LDS, so every item's length (the distance to
+// the next start) is written without reading global memory back; the last
+// item of a pass is closed by the next pass's first start (or R).  Every run
+// start is a block start, so the items tile the rows in order; unsorted
+// indices only give shorter runs.
 __global__ void __launch_bounds__(1024) qmm_segments_kernel(const uint32_t* __restrict__ idx, int R, int BM,
                                                             int32_t* seg) {
-  constexpr int STAGE = 16384;  // rows staged per load phase (all loads of a phase in flight at once)
-  __shared__ uint32_t sidx[STAGE + 128];
+  constexpr int RPT = 4, PASS = 1024 * RPT;
+  __shared__ int istart[PASS];  // this pass's item starts, in order
   __shared__ int wmax[16], wsum[16];
-  __shared__ int carry_start, carry_count;
+  __shared__ int carry_start, carry_count, last_start, pass_items;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  if (tid == 0) carry_start = 0, carry_count = 0;
-  for (int base0 = 0; base0 < R; base0 += STAGE) {
-  const int nst = min(STAGE + BM, R - base0);  // every index a chunk below can read
-#pragma unroll 8
-  for (int i = tid; i < nst; i += 1024) sidx[i] = idx[base0 + i];
-  const uint32_t before0 = base0 > 0 ? idx[base0 - 1] : 0u;
+  if (tid == 0) carry_start = 0, carry_count = 0, last_start = 0;
   __syncthreads();
-  for (int cb = 0; cb < STAGE && base0 + cb < R; cb += 1024) {
-    const int base = base0 + cb, loc = cb + tid;
-    const int r = base + tid;
-    const bool valid = r < R;
-    const uint32_t cur = sidx[loc];
-    const bool st = valid && (r == 0 || (loc > 0 ? sidx[loc - 1] : before0) != cur);
-    int v = st ? r : -1;  // inclusive max-scan: latest run start at or before r
-    int c;
+  for (int base = 0; base < R; base += PASS) {
+    const int r0 = base + RPT * tid;
+    uint32_t v[RPT];
+#pragma unroll
+    for (int k = 0; k < RPT; k++) v[k] = r0 + k < R ? idx[r0 + k] : 0u;
+    const uint32_t before = r0 > 0 && r0 <= R ? idx[r0 - 1] : 0u;
+    // latest run start at or before each of this thread's rows (-1: none yet)
+    int ls[RPT], cur = -1;
+#pragma unroll
+    for (int k = 0; k < RPT; k++) {
+      const int r = r0 + k;
+      if (r < R && (r == 0 || (k ? v[k - 1] : before) != v[k])) cur = r;
+      ls[k] = cur;
+    }
+    int m = cur;  // inclusive max-scan over the threads
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
-      const int o = __shfl_up(v, off);
-      if (lane >= off) v = max(v, o);
+      const int o = __shfl_up(m, off);
+      if (lane >= off) m = max(m, o);
     }
-    if (lane == 63) wmax[wave] = v;
+    if (lane == 63) wmax[wave] = m;
     __syncthreads();
-    for (int w = 0; w < wave; w++) v = max(v, wmax[w]);
-    const int rs = v >= 0 ? v : carry_start;
-    const bool f = valid && (r - rs) % BM == 0;  // a block starts here
-    c = f ? 1 : 0;  // inclusive sum-scan of block starts
+    int prior = carry_start;  // run start carried into this thread's first row
+    for (int w = 0; w < wave; w++) prior = max(prior, wmax[w]);
+    const int up = __shfl_up(m, 1);
+    if (lane > 0) prior = max(prior, up);
+    int nf = 0;
+    bool f[RPT];
+#pragma unroll
+    for (int k = 0; k < RPT; k++) {
+      const int r = r0 + k;
+      const int rs = ls[k] >= 0 ? ls[k] : prior;
+      f[k] = r < R && (r - rs) % BM == 0;  // a block starts here
+      nf += f[k] ? 1 : 0;
+    }
+    int c = nf;  // inclusive sum-scan of block starts over the threads
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
       const int o = __shfl_up(c, off);
@@ -943,31 +958,37 @@ __global__ void __launch_bounds__(1024) qmm_segments_kernel(const uint32_t* __re
     if (lane == 63) wsum[wave] = c;
     __syncthreads();
     for (int w = 0; w < wave; w++) c += wsum[w];
-    if (f) {  // rows of the item: set below from the next item's start
-      const int pos = carry_count + c - 1;
-      seg[1 + 3 * pos] = r;
-      seg[3 + 3 * pos] = (int32_t)cur;
+    int pos = c - nf;  // this thread's first item in the pass
+    const int cc = carry_count;
+#pragma unroll
+    for (int k = 0; k < RPT; k++) {
+      if (f[k]) {
+        istart[pos] = r0 + k;
+        seg[1 + 3 * (cc + pos)] = r0 + k;
+        seg[3 + 3 * (cc + pos)] = (int32_t)v[k];
+        pos++;
+      }
     }
-    const int last = min(R - base, 1024) - 1;  // this chunk's last valid row
-    int total = 0;
-    if (tid == last)
-      for (int w = 0; w < 16; w++) total += wsum[w];
-    __syncthreads();  // every thread is done with carry_*, wmax and wsum
-    if (tid == last) {
-      carry_start = rs;
-      carry_count += total;
+    if (tid == 1023) {
+      pass_items = c;
+      int mx = carry_start;
+      for (int w = 0; w < 16; w++) mx = max(mx, wmax[w]);
+      carry_start = mx;  // read by no thread before the barrier below
+    }
+    __syncthreads();
+    const int total = pass_items;
+    for (int jj = tid; jj + 1 < total; jj += 1024) seg[2 + 3 * (cc + jj)] = istart[jj + 1] - istart[jj];
+    if (tid == 0 && total > 0) {
+      if (cc > 0) seg[2 + 3 * (cc - 1)] = istart[0] - last_start;  // the previous pass's last item
+      last_start = istart[total - 1];
+      carry_count = cc + total;
     }
     __syncthreads();
   }
-  }  // load phases (the last chunk's barrier also covers the reads of sidx)
-  // Every run start is a block start, so the items tile the rows in order:
-  // an item ends where the next one starts (the workgroup's own global
-  // writes are visible to it after the barrier).
-  __threadfence_block();
-  __syncthreads();
-  const int count = carry_count;
-  for (int j = tid; j < count; j += 1024) seg[2 + 3 * j] = (j + 1 < count ? seg[1 + 3 * (j + 1)] : R) - seg[1 + 3 * j];
-  if (tid == 0) seg[0] = count;
+  if (tid == 0) {
+    if (carry_count > 0) seg[2 + 3 * (carry_count - 1)] = R - last_start;
+    seg[0] = carry_count;
+  }
 }
 
 // y = T(sum over splits of the fp32 partials), fixed split order.
@@ -1402,7 +1423,7 @@ template <typename T, int BITS, int GS, int BM>
 int launch_qmm_sorted_inst(const void* x, int64_t R, int64_t K, const uint32_t* w, const void* scales,
                            const void* biases, const uint32_t* idx, int64_t n_experts, int64_t N, void* y,
                            hipStream_t s) {
-  static_assert(BM <= 128, "qmm_segments_kernel stages BM indices past each chunk");
+  static_assert(BM >= 1 && BM <= 128, "work-list block rows");
   void* p = nullptr;
   int rc = mlxq::workspace((1 + 3 * (size_t)R) * sizeof(int32_t), &p, s);
   if (rc) return rc;

@@ -358,21 +358,27 @@ def experts_many(O):
     return wq, wd
 
 
-@pytest.mark.parametrize("rows,experts", [(16384, "few"), (16384, "many"), (20000, "few"), (20000, "many")])
+@pytest.mark.parametrize("rows,experts", [(16384, "few"), (16384, "many"), (20000, "few"), (20000, "many"),
+                                          (4106, "few"), (4106, "many")])
 def test_gather_qmm_sorted_past_one_index_stage(O, mlxq_dev, experts_small, experts_many, rows, experts):
-    """The segments kernel stages 16384 indices per load phase: 16384 rows
-    (the reference's 2048-token prefill chunk x top-8) end exactly on the
-    stage boundary, 20000 rows cross it with one expert's run straddling row
-    16384 (its carry across phases).  16 experts give 64-row blocks, 512
-    experts 32-row blocks.  Against the fp64 reference and the per-row
-    gather."""
+    """The segments kernel builds the work list 4096 rows a pass: 16384 rows
+    (the reference's 2048-token prefill chunk x top-8) end exactly on a pass
+    boundary, 20000 rows have one expert's run straddling row 16384 (its run
+    start and open item carried into the next pass), and 4106 rows end in a
+    10-row pass inside a run that starts no block there (a pass with no item
+    of its own).  16 experts give 64-row blocks, 512 experts 32-row blocks.
+    Against the fp64 reference and the per-row gather."""
     wq, wd = experts_small if experts == "few" else experts_many
     E, K = wd.shape[0], wd.shape[2]
     r = np.random.default_rng(rows + E)
     idx = np.sort(r.integers(0, E, rows)).astype(np.uint32)
-    if rows > 16384:
-        idx[16360:16410] = idx[16360]  # one run across the stage boundary (order kept)
+    if rows == 20000:
+        idx[16360:16410] = idx[16360]  # one run across the pass boundary (order kept)
         assert idx[16383] == idx[16384]
+    if rows == 4106:
+        idx[-30:] = E - 1  # one run from row 4076: its next block would start at 4108
+        idx[:-30] = np.minimum(idx[:-30], E - 2)
+        idx.sort()
     x = rng_t(O, (rows, 1, K), 90 + rows, BF16)
     got = _gather(O, x, wq, idx, 64, 4, BF16, sorted_indices=True)
     assert_close(got, _sorted_ref(x, wd, idx), what=f"sorted gather {rows} rows, {E} experts", dtype=BF16)
