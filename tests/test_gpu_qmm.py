@@ -63,22 +63,26 @@ def test_qmv_qmm_down_proj(O, mlxq_dev, w_down, M):
     assert_close(y, x.astype(np.float64) @ wd.T, what=f"down M={M}", dtype=BF16)
 
 
-@pytest.mark.parametrize("dtype,N,K", [
-    (BF16, 1000, 2048),   # ragged N
-    (F16, 333, 2816),     # 22 tiles (the tied-head and MoE gate_up K)
-    (BF16, 77, 14336),    # 112 tiles
-    (F16, 4097, 6144),    # one row past a workgroup multiple
-    (BF16, 9, 3072),      # fewer rows than one row tile
-    (F16, 50, 1280),      # 10 tiles
+@pytest.mark.parametrize("dtype,M,N,K", [
+    (BF16, 1, 1000, 2048),   # ragged N
+    (F16, 1, 333, 2816),     # 22 tiles (the tied-head and MoE gate_up K)
+    (BF16, 1, 77, 14336),    # 112 tiles
+    (F16, 1, 4097, 6144),    # one row past a workgroup multiple
+    (BF16, 1, 9, 3072),      # fewer rows than one row tile
+    (F16, 1, 50, 1280),      # 10 tiles
+    (BF16, 2, 1000, 2048),   # two activation rows
+    (F16, 2, 333, 2816),
+    (BF16, 2, 4097, 14336),
 ])
-def test_qmv_one_row_shapes(O, mlxq_dev, dtype, N, K):
-    """One activation row (qmv, 4-bit, group 64) against the float64
-    reference: K from 10 to 112 tiles, ragged N, fewer rows than a workgroup."""
+def test_qmv_one_row_shapes(O, mlxq_dev, dtype, M, N, K):
+    """One or two activation rows (qmv, 4-bit, group 64) against the float64
+    reference: K from 10 to 112 tiles of 128 codes (a clamped duplicate tail
+    at 22), ragged N, fewer rows than a row tile."""
     w = rng_t(O, (N, K), 13, dtype, 0.05)
     wq = O.quantize(w, 64, 4, dtype)
-    x = rng_t(O, (1, K), 14, dtype)
+    x = rng_t(O, (M, K), 14, dtype)
     y = run_qmm(O, mlxq_dev, x, wq, 64, 4, dtype)
-    assert_close(y, x.astype(np.float64) @ deq64(O, *wq, 64, 4, dtype).T, what="dot", dtype=dtype)
+    assert_close(y, x.astype(np.float64) @ deq64(O, *wq, 64, 4, dtype).T, what="qmv", dtype=dtype)
 
 
 @pytest.mark.parametrize("dtype,bits,gs,M,N,K", [
