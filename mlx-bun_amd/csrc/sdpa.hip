@@ -126,11 +126,23 @@ struct ChunkRange {
 // `chunk` is a power of two (the launchers only halve it from one), so the
 // divisions are shifts: 64-bit division would expand to a few hundred
 // instructions ahead of every workgroup's first load.
+// A ring row whose window fills the ring attends every slot, and a decode
+// chunk's keys may come in any order (softmax and the chunk merge do not
+// depend on it), so such a row is cut at physical slots: ceil(cap / chunk)
+// whole chunks instead of a short leading chunk, whole chunks and a short
+// trailing one (one workgroup less per row when the write index is not
+// chunk-aligned).
 __device__ __forceinline__ ChunkRange chunk_range(const Geometry& geo, int b, int chunk, int c) {
   ChunkRange r;
   const int sh = __builtin_ctz((unsigned)chunk);
   const int64_t cm = chunk - 1;
   const int64_t valid = row_valid(geo, b);
+  if (geo.ring_off && valid == geo.cap) {
+    r.nch = (int)((geo.cap + cm) >> sh);
+    r.j0 = r.slot0 = (int64_t)c * chunk;
+    r.nk = (int)min((int64_t)chunk, geo.cap - r.slot0);
+    return r;
+  }
   const int64_t base = row_base_slot(geo, b, valid);  // in [0, cap)
   const int64_t jw = geo.cap - base;                  // first logical key stored at slot 0
   const int64_t off = jw < valid ? (jw & cm) : 0;     // length of a leading short chunk (0: none)
