@@ -179,17 +179,19 @@ __device__ __forceinline__ float xrow_sum(float v) {
 #define MLXQ_DECODE_WINDOW 2
 #endif
 
-// Decode tile geometry for one (T, BITS, D, GS) instance.
-template <int BITS, int D, int GS>
+// Decode tile geometry for one (T, BITS, D, GS) instance with NWV waves a
+// workgroup.  The chunk (MAXC keys) does not depend on NWV: 4 waves take
+// twice the tiles of 8.
+template <int BITS, int D, int GS, int NWV = 8>
 struct DecodeShape {
-  static constexpr int NW = 8;               // waves per workgroup
+  static constexpr int NW = NWV;             // waves per workgroup
   static constexpr int KW = D * BITS / 32;   // packed words per cache row
   static constexpr int G = D / GS;
-  // tiles (32 keys) per wave: up to 128/KW, with the chunk's fp32
-  // scales/biases (16 G bytes per key) held to 32 KB of LDS, 64 KB from 4
-  // groups a row on (D 256 at group 64: 4 tiles a wave instead of 2, half the
-  // chunks; the 32-row batched ring decode 102 -> 86 us on MI355X)
-  static constexpr int TPW_REG = 128 / KW;
+  // tiles (32 keys) per wave: up to 1024/KW a workgroup, with the chunk's
+  // fp32 scales/biases (16 G bytes per key) held to 32 KB of LDS, 64 KB from
+  // 4 groups a row on (D 256 at group 64: 4 tiles a wave of 8 instead of 2,
+  // half the chunks; the 32-row batched ring decode 102 -> 86 us on MI355X)
+  static constexpr int TPW_REG = 1024 / (KW * NW);
   static constexpr int TPW_LDS = (G >= 4 ? 4096 : 2048) / (G * NW * 32);
   static constexpr int TPW = TPW_REG < TPW_LDS ? TPW_REG : TPW_LDS;
   static constexpr int MAXC = NW * 32 * TPW;  // keys per workgroup
@@ -205,20 +207,24 @@ struct DecodeShape {
 };
 
 // One workgroup = NW waves = one chunk of up to MAXC keys of one (batch row,
-// kv head).  Wave w owns the 32-key tiles w + NW t, t < TPW.  Each wave loads
-// its own tiles' scales/biases first and stages them in its LDS region as
-// fp32 (per-key constants folded in once per key, not once per MFMA column;
-// no workgroup barrier, so a wave starts on its first tile as soon as its own
-// data is in); codes stream through a WIN-tile register window: tile t + WIN
-// is requested as soon as tile t is consumed.
-template <typename T, int BITS, int D, int GS>
-__global__ void __launch_bounds__(512) sdpa_decode_mfma_kernel(
+// kv head).  NW = 8, or 4 where a launch has several workgroups a CU and
+// the kernel needs more than 128 VGPRs: two 4-wave workgroups then share a
+// CU where only one 8-wave workgroup would fit, so one streams while the
+// other starts or finishes.  Wave w owns the 32-key tiles w + NW t,
+// t < TPW.  Each wave loads its own tiles' scales/biases first and stages
+// them in its LDS region as fp32 (per-key constants folded in once per key,
+// not once per MFMA column; no workgroup barrier, so a wave starts on its
+// first tile as soon as its own data is in); codes stream through a
+// WIN-tile register window: tile t + WIN is requested as soon as tile t is
+// consumed.
+template <typename T, int BITS, int D, int GS, int NWV>
+__global__ void __launch_bounds__(NWV * 64, 2) sdpa_decode_mfma_kernel(
     const uint16_t* __restrict__ q, const uint32_t* __restrict__ kp, const uint16_t* __restrict__ ksc,
     const uint16_t* __restrict__ kbi, const uint32_t* __restrict__ vp, const uint16_t* __restrict__ vsc,
     const uint16_t* __restrict__ vbi, int Hq, int Hkv, Geometry geo, float scale, int chunk,
     uint16_t* __restrict__ out, float* __restrict__ part_o, float2* __restrict__ part_ml) {
   using CO = CodeOps<T, BITS>;
-  using SH = DecodeShape<BITS, D, GS>;
+  using SH = DecodeShape<BITS, D, GS, NWV>;
   constexpr int NW = SH::NW, TPW = SH::TPW, G = SH::G, KW = SH::KW, WIN = SH::WIN;
   constexpr int NT = NW * 64;
   constexpr int GW = (G + 1) / 2;    // dwords holding one row's G group values
@@ -232,7 +238,7 @@ __global__ void __launch_bounds__(512) sdpa_decode_mfma_kernel(
   constexpr float OFF = CO::OFFSET;  // code operands carry +OFF (K and V alike)
   static_assert(VM * E == DT, "tile bookkeeping");
   static_assert(LKW % 4 == 0, "K quarter rows are whole dwordx4 loads");
-  static_assert(NT == 512, "launch bounds");
+  static_assert(NT == NWV * 64, "launch bounds");
 
   // sb_lds[wave]: [0] K scale * log2e, [1] (K bias - OFF * K scale) * log2e,
   // [2] V scale, [3] V bias -- per group, for the wave's own keys (tile t at
@@ -2036,15 +2042,17 @@ int launch_decode(const void* q, int B, int Hq, int Hkv, const uint32_t* kp, con
                   const uint32_t* vp, const void* vs, const void* vb, Geometry geo, float scale, void* out,
                   hipStream_t s, const mlxq::Scratch& scr) {
   using SH = DecodeShape<BITS, D, GS>;
+  using SH4 = DecodeShape<BITS, D, GS, 4>;
   constexpr int MAXC = SH::MAXC;
+  static_assert(SH4::MAXC == MAXC, "the chunk does not depend on the wave count");
   MLXQ_CHECK(geo.cap * (int64_t)SH::KW * 4 < ((int64_t)1 << 31), "kv cache rows too long for one launch");
+  const int64_t cus = mlxq::device_cu_count();
   const int64_t span = geo.valid_len ? geo.cap : geo.n_kv;  // per-row upper bound on keys
   int chunk = MAXC;
   const int ov = decode_chunk_override();
   if (ov >= 32 && ov <= MAXC && (ov & (ov - 1)) == 0) {
     chunk = ov;
   } else {
-    const int64_t cus = mlxq::device_cu_count();
     while (chunk > 128 && ((span + chunk - 1) / chunk) * B * Hkv < cus) chunk /= 2;
   }
   // a ring row's window may start mid-chunk at the wrap point: one extra chunk
@@ -2063,10 +2071,27 @@ int launch_decode(const void* q, int B, int Hq, int Hkv, const uint32_t* kp, con
   float* part_o = (float*)pws;
   float2* part_ml = pbytes ? (float2*)((uint8_t*)pws + obytes) : nullptr;
   dim3 grid((unsigned)nchunks, (unsigned)Hkv, (unsigned)B);
-  hipLaunchKernelGGL((sdpa_decode_mfma_kernel<T, BITS, D, GS>), grid, dim3(SH::NW * 64), 0, s, (const uint16_t*)q,
-                     kp, (const uint16_t*)ks, (const uint16_t*)kb, vp, (const uint16_t*)vs, (const uint16_t*)vb, Hq,
-                     Hkv, geo, scale, chunk, (uint16_t*)out, part_o, part_ml);
-  MLXQ_LAUNCHED("sdpa_decode_mfma_kernel");
+  // 4-bit D 256 (200+ VGPRs: one 8-wave workgroup a CU) with at least two
+  // workgroups a CU: 4-wave workgroups, two a CU (the 32-row batched ring
+  // decode, 1280 workgroups: 84-88 -> 67-73 us on MI355X, one box)
+  if constexpr (BITS == 4 && D == 256) {
+    if (slots >= 2 * (size_t)cus) {
+      hipLaunchKernelGGL((sdpa_decode_mfma_kernel<T, BITS, D, GS, 4>), grid, dim3(SH4::NW * 64), 0, s,
+                         (const uint16_t*)q, kp, (const uint16_t*)ks, (const uint16_t*)kb, vp, (const uint16_t*)vs,
+                         (const uint16_t*)vb, Hq, Hkv, geo, scale, chunk, (uint16_t*)out, part_o, part_ml);
+      MLXQ_LAUNCHED("sdpa_decode_mfma_kernel");
+    } else {
+      hipLaunchKernelGGL((sdpa_decode_mfma_kernel<T, BITS, D, GS, 8>), grid, dim3(SH::NW * 64), 0, s,
+                         (const uint16_t*)q, kp, (const uint16_t*)ks, (const uint16_t*)kb, vp, (const uint16_t*)vs,
+                         (const uint16_t*)vb, Hq, Hkv, geo, scale, chunk, (uint16_t*)out, part_o, part_ml);
+      MLXQ_LAUNCHED("sdpa_decode_mfma_kernel");
+    }
+  } else {
+    hipLaunchKernelGGL((sdpa_decode_mfma_kernel<T, BITS, D, GS, 8>), grid, dim3(SH::NW * 64), 0, s, (const uint16_t*)q,
+                       kp, (const uint16_t*)ks, (const uint16_t*)kb, vp, (const uint16_t*)vs, (const uint16_t*)vb, Hq,
+                       Hkv, geo, scale, chunk, (uint16_t*)out, part_o, part_ml);
+    MLXQ_LAUNCHED("sdpa_decode_mfma_kernel");
+  }
   if (nchunks > 1) {
     const int cols = nrep * D / 4;
     dim3 mgrid((unsigned)((cols + 63) / 64), (unsigned)Hkv, (unsigned)B);

@@ -132,6 +132,16 @@ def test_decode_wide(O, mlxq_dev, B, Hq, Hkv, N, D, gs, bits, dtype, scale):
     check(O, run(O, mlxq_dev, q, kq, vq, dtype, scale, gs, bits), q, kq, vq, dtype, scale, gs, bits, "wide")
 
 
+@pytest.mark.parametrize("gs,dtype", [(64, F16), (32, BF16), (128, BF16)])
+def test_decode_d256_four_wave_workgroups(O, mlxq_dev, gs, dtype):
+    """4-bit D 256 with 512 key chunks in the launch (8 rows x 8 kv heads x
+    8 chunks of 1024 keys): two or more workgroups a CU on a 256-CU part, so
+    the launcher takes 4-wave workgroups with 8 tiles a wave.  Scale 1 (the
+    most peaked softmax), every group size."""
+    q, kq, vq = case(O, 8, 16, 8, 1, 8192, 256, gs, 4, dtype, 40 + gs)
+    check(O, run(O, mlxq_dev, q, kq, vq, dtype, 1.0, gs, 4), q, kq, vq, dtype, 1.0, gs, 4, f"d256 gs{gs}")
+
+
 def test_decode_wide_ring(O, mlxq_dev):
     """Rotating rows at the Gemma4 full-attention shape: per-row valid lengths
     (short, one short of the ring, full, wrapped past it) and ring offsets."""
