@@ -1291,6 +1291,10 @@ int launch_qmv_inst(const void* x, int64_t batch, int64_t M, int64_t K, const ui
   }
 }
 
+// launch_qmv's result when no qmv instance matches the plan (no error is
+// set): the dispatch then takes the next kernel that accepts the shape
+constexpr int QMV_NONE = -1;
+
 template <typename T, int BITS, int GS>
 int launch_qmv(const void* x, int64_t batch, int64_t M, int64_t K, const uint32_t* w, const void* scales,
                const void* biases, const BatchMap& bm, int64_t N, void* y, const QmvPlan& p, hipStream_t s) {
@@ -1305,7 +1309,7 @@ int launch_qmv(const void* x, int64_t batch, int64_t M, int64_t K, const uint32_
   QMV_I(1, 1, 16, 4, 16) QMV_I(1, 2, 16, 4, 16) QMV_I(1, 1, 8, 4, 16) QMV_I(1, 2, 8, 4, 16)
   QMV_I(2, 1, 4, 4, 16) QMV_I(2, 2, 4, 4, 16) QMV_I(2, 1, 8, 4, 16) QMV_I(2, 2, 8, 4, 16)
 #undef QMV_I
-  return mlxq::fail(MLXQ_ERR_UNSUPPORTED, "qmv: no instance for this plan");
+  return QMV_NONE;
 }
 
 // Kernel choice shared by quantized_matmul and gather_qmm: qmv for small M,
@@ -1320,18 +1324,22 @@ int qmm_dispatch(const void* x, int dtype, int64_t batch, int64_t M, int64_t K, 
                       K * M < ((int64_t)1 << 30) && batch < 65536 &&
                       plan_qmv(bits, group_size, M, K, N, batch, &plan);
   if (qmv_ok) {
+    int rc;
     if (dtype == MLXQ_BFLOAT16) {
       if (bits == 4)
-        return group_size == 64 ? launch_qmv<BF16, 4, 64>(x, batch, M, K, w, scales, biases, bm, N, y, plan, s)
-                                : launch_qmv<BF16, 4, 128>(x, batch, M, K, w, scales, biases, bm, N, y, plan, s);
-      return group_size == 64 ? launch_qmv<BF16, 8, 64>(x, batch, M, K, w, scales, biases, bm, N, y, plan, s)
+        rc = group_size == 64 ? launch_qmv<BF16, 4, 64>(x, batch, M, K, w, scales, biases, bm, N, y, plan, s)
+                              : launch_qmv<BF16, 4, 128>(x, batch, M, K, w, scales, biases, bm, N, y, plan, s);
+      else
+        rc = group_size == 64 ? launch_qmv<BF16, 8, 64>(x, batch, M, K, w, scales, biases, bm, N, y, plan, s)
                               : launch_qmv<BF16, 8, 128>(x, batch, M, K, w, scales, biases, bm, N, y, plan, s);
-    }
-    if (bits == 4)
-      return group_size == 64 ? launch_qmv<F16, 4, 64>(x, batch, M, K, w, scales, biases, bm, N, y, plan, s)
-                              : launch_qmv<F16, 4, 128>(x, batch, M, K, w, scales, biases, bm, N, y, plan, s);
-    return group_size == 64 ? launch_qmv<F16, 8, 64>(x, batch, M, K, w, scales, biases, bm, N, y, plan, s)
+    } else if (bits == 4) {
+      rc = group_size == 64 ? launch_qmv<F16, 4, 64>(x, batch, M, K, w, scales, biases, bm, N, y, plan, s)
+                            : launch_qmv<F16, 4, 128>(x, batch, M, K, w, scales, biases, bm, N, y, plan, s);
+    } else {
+      rc = group_size == 64 ? launch_qmv<F16, 8, 64>(x, batch, M, K, w, scales, biases, bm, N, y, plan, s)
                             : launch_qmv<F16, 8, 128>(x, batch, M, K, w, scales, biases, bm, N, y, plan, s);
+    }
+    if (rc != QMV_NONE) return rc;
   }
 
   // 4-bit group 64, M <= 64 (the shapes qmv does not take): the

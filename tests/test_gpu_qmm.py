@@ -85,6 +85,25 @@ def test_qmv_one_row_shapes(O, mlxq_dev, dtype, M, N, K):
     assert_close(y, x.astype(np.float64) @ deq64(O, *wq, 64, 4, dtype).T, what="qmv", dtype=dtype)
 
 
+@pytest.mark.parametrize("dtype,gs,M,N,K", [
+    (BF16, 128, 12, 1000, 4096),  # 12 rows at group 128: a qmv plan with no compiled instance
+    (F16, 128, 16, 15000, 512),   # the same at 16 rows, ragged N
+    (BF16, 64, 1, 5000, 1024),
+    (F16, 64, 4, 9000, 2048),
+    (F16, 64, 2, 12345, 4096),    # odd N
+])
+def test_qmm_small_m_shapes(O, mlxq_dev, dtype, gs, M, N, K):
+    """Small-M shapes against float64, among them 9-16 activation rows at
+    group 128 (one MFMA row block with 16-chunk x staging): the qmv plan for
+    them has no compiled instance, and the call must go on to the tiled GEMM
+    rather than fail."""
+    w = rng_t(O, (N, K), 15, dtype, 0.05)
+    wq = O.quantize(w, gs, 4, dtype)
+    x = rng_t(O, (M, K), 16, dtype)
+    y = run_qmm(O, mlxq_dev, x, wq, gs, 4, dtype)
+    assert_close(y, x.astype(np.float64) @ deq64(O, *wq, gs, 4, dtype).T, what="small M", dtype=dtype)
+
+
 @pytest.mark.parametrize("dtype,bits,gs,M,N,K", [
     (F16, 4, 64, 3, 200, 512),
     (F16, 8, 64, 5, 130, 768),
