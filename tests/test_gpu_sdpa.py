@@ -80,6 +80,22 @@ def test_decode_batched_ring_window(O, mlxq_dev):
     check(O, got, q, kq, vq, BF16, 1.0, 64, 4, "c3", valid_len=lens, ring_off=ring)
 
 
+@pytest.mark.parametrize("gs,dtype", [(32, F16), (128, BF16)])
+def test_decode_ring_four_wave_workgroups(O, mlxq_dev, gs, dtype):
+    """Rotating rows on the 4-wave decode workgroups (4-bit D 256, 16 rows x
+    8 kv heads x 9 chunks of a 8192-slot ring: two or more workgroups a CU
+    on a 256-CU part) at group sizes 32 and 128: short rows, full rings cut
+    at physical slots, and wrapped windows."""
+    r = np.random.default_rng(gs)
+    B, W = 16, 8192
+    lens = r.integers(100, 20000, B).astype(np.int32)
+    lens[:4] = [1, 8191, 8192, 8193]
+    ring = r.integers(0, W, B).astype(np.int32)
+    q, kq, vq = case(O, B, 16, 8, 1, W, 256, gs, 4, dtype, 60 + gs)
+    got = run(O, mlxq_dev, q, kq, vq, dtype, 0.0625, gs, 4, valid=lens, ring=ring)
+    check(O, got, q, kq, vq, dtype, 0.0625, gs, 4, f"ring gs{gs}", valid_len=lens, ring_off=ring)
+
+
 @pytest.mark.parametrize("Hq,Hkv,D", [(32, 8, 128), (16, 8, 256)])
 def test_decode_32k_scale_one(O, mlxq_dev, Hq, Hkv, D):
     """Gemma4 calls quantizedSdpa with scale 1 (src/model/gemma4-base.ts:1282-1285):
