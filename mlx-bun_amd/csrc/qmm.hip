@@ -344,8 +344,12 @@ __global__ void __launch_bounds__(512) qmv_kernel(const uint16_t* __restrict__ x
 template <int MB>
 struct DmaShape {
   static constexpr int WB = 4;                   // K tiles per weight batch (256 bytes of a row)
-  static constexpr int NSB = MB >= 3 ? 3 : MB == 2 ? 4 : 5;  // weight ring slots (batches)
-  static constexpr int NSX = MB == 4 ? 6 : 8;    // x ring slots (K tiles)
+  // weight ring slots (batches) and x ring slots (K tiles); at MB = 4 the
+  // x ring gives two slots to the weights (M = 64 on MI355X: 25.4-26.0 ->
+  // 24.9 us up, 27.5-27.7 -> 27.2 down; 5 weight batches and 4 x slots, or
+  // deeper weight rings at MB = 1, measured the same or slower)
+  static constexpr int NSB = MB == 4 ? 4 : MB == 3 ? 3 : MB == 2 ? 4 : 5;
+  static constexpr int NSX = MB == 4 ? 4 : 8;
   static constexpr int WSLOT = 16 * 1024;        // codes of a batch: 64 rows x 256 bytes
   static constexpr int SSLOT = 2 * 1024;         // scales, biases of a batch
   static constexpr int XSLOT = MB * 4 * 1024;    // x of a K tile: MB row blocks x 16 rows x 256 bytes
