@@ -73,7 +73,7 @@ __global__ void __launch_bounds__(512) qmv_kernel(const uint16_t* __restrict__ x
                                                   const uint32_t* __restrict__ w,
                                                   const uint16_t* __restrict__ scales,
                                                   const uint16_t* __restrict__ biases, int N, BatchMap bm,
-                                                  uint16_t* __restrict__ y) {
+                                                  int RW, uint16_t* __restrict__ y) {
   using CO = CodeOps<T, BITS>;
   constexpr int TILE_K = 512 / BITS;                 // codes per 64-byte row segment
   constexpr int KS = TILE_K / 32;                    // MFMA k-steps per tile
@@ -95,8 +95,11 @@ __global__ void __launch_bounds__(512) qmv_kernel(const uint16_t* __restrict__ x
   int64_t xb, wb;
   bool xok, wok;
   bm.resolve(bidx, xb, xok, wb, wok);
-  const int n0 = blockIdx.x * 16 * R;
-  const int rows = wok ? min(16 * R, N - n0) : 0;
+  // RW <= 16 R weight rows a workgroup: rows of its last tile past RW read
+  // 0 past the descriptors and are not stored
+  const int n0 = blockIdx.x * RW;
+  const int nrow = min(RW, N - n0);
+  const int rows = wok ? nrow : 0;
   const int G = K / GS, KT = (K + TILE_K - 1) / TILE_K;
   const uint32_t row_bytes = (uint32_t)K * BITS / 8;
   x += xb * M * K;
@@ -300,7 +303,7 @@ __global__ void __launch_bounds__(512) qmv_kernel(const uint16_t* __restrict__ x
       float v = 0.f;
 #pragma unroll
       for (int q = 0; q < QG; q++) v += acc[i + q];
-      if (m < M && n < N) y[(int64_t)m * N + n] = (uint16_t)Conv<T>::to_bits(v);
+      if (m < M && 16 * ri + ln < nrow) y[(int64_t)m * N + n] = (uint16_t)Conv<T>::to_bits(v);
     }
   }
 }
@@ -1200,6 +1203,7 @@ __global__ void __launch_bounds__(256) qmm_generic_kernel(const void* __restrict
 // it (then the general kernels run).
 struct QmvPlan {
   int R, TPW, NW, MB, MR, XC;  // XC: x chunks (8 values) each lane stages, 8 or 16
+  int RW;                      // weight rows a workgroup (<= 16 R)
   size_t lds;
 };
 
@@ -1216,6 +1220,15 @@ int qmv_r_override() {
   static const int v = [] {
     const char* e = getenv("MLXQ_QMV_R");
     return e ? atoi(e) : 0;
+  }();
+  return v;
+}
+// MLXQ_QMV_EVEN=0 keeps 16 rows a workgroup where fewer would even out the
+// workgroups a CU.
+int qmv_even_override() {
+  static const int v = [] {
+    const char* e = getenv("MLXQ_QMV_EVEN");
+    return e ? atoi(e) : 1;
   }();
   return v;
 }
@@ -1262,6 +1275,21 @@ bool plan_qmv(int bits, int gs, int64_t M, int64_t K, int64_t N, int64_t batch, 
     }
   }
   if (qmv_r_override() == 1 || qmv_r_override() == 2) p->R = qmv_r_override();
+  p->RW = 16 * p->R;
+  // One matrix, one row tile a workgroup, and a tile count that is not a
+  // whole number a CU (x[1, 4096] @ W[14336, 4096]^T: 896 tiles, 3.5 a CU --
+  // the CUs that took a fourth workgroup finished last): as many rows a
+  // workgroup as give a whole number a CU, down to 12 (the tile's other rows
+  // are masked).  MI355X: 9.20 -> 9.04 us; the MoE gather (8 matrices) was
+  // 1 % slower with it, so batches keep 16 rows.
+  if (p->R == 1 && batch == 1 && qmv_even_override() != 0) {
+    const int64_t tiles = (N + 15) / 16;
+    if (tiles > cus && tiles % cus != 0) {
+      const int64_t k = (tiles + cus - 1) / cus;  // workgroups a CU
+      const int64_t rw = (N + k * cus - 1) / (k * cus);
+      if (rw >= 12 && rw < 16) p->RW = (int)rw;
+    }
+  }
   p->NW = (int)((kt + p->TPW - 1) / p->TPW);
   const int64_t xpw = (int64_t)p->TPW * tile_k, ngw = xpw / gs;
   const size_t wave_lds = (size_t)M * xpw * 2 + (size_t)ngw * 16 * p->R * 8;
@@ -1287,9 +1315,10 @@ int launch_qmv_inst(const void* x, int64_t batch, int64_t M, int64_t K, const ui
         raised = true;
       }
     }
-    dim3 grid((unsigned)((N + 16 * R - 1) / (16 * R)), (unsigned)batch);
+    MLXQ_CHECK(p.RW >= 1 && p.RW <= 16 * R, "qmv: rows per workgroup");
+    dim3 grid((unsigned)((N + p.RW - 1) / p.RW), (unsigned)batch);
     hipLaunchKernelGGL(kern, grid, dim3(p.NW * 64), p.lds, s, (const uint16_t*)x, (int)M, (int)K, w,
-                       (const uint16_t*)scales, (const uint16_t*)biases, (int)N, bm, (uint16_t*)y);
+                       (const uint16_t*)scales, (const uint16_t*)biases, (int)N, bm, p.RW, (uint16_t*)y);
     MLXQ_LAUNCHED("qmv_kernel");
     return MLXQ_OK;
   }
