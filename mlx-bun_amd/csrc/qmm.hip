@@ -1276,18 +1276,22 @@ bool plan_qmv(int bits, int gs, int64_t M, int64_t K, int64_t N, int64_t batch, 
   }
   if (qmv_r_override() == 1 || qmv_r_override() == 2) p->R = qmv_r_override();
   p->RW = 16 * p->R;
-  // One matrix, one row tile a workgroup, and a tile count that is not a
-  // whole number a CU (x[1, 4096] @ W[14336, 4096]^T: 896 tiles, 3.5 a CU --
+  // One matrix, one row tile a workgroup, and a workgroup count that is not
+  // a whole number a CU (x[1, 4096] @ W[14336, 4096]^T: 896 tiles, 3.5 a CU --
   // the CUs that took a fourth workgroup finished last): as many rows a
   // workgroup as give a whole number a CU, down to 12 (the tile's other rows
   // are masked).  MI355X: 9.20 -> 9.04 us; the MoE gather (8 matrices) was
   // 1 % slower with it, so batches keep 16 rows.
-  if (p->R == 1 && batch == 1 && qmv_even_override() != 0) {
-    const int64_t tiles = (N + 15) / 16;
-    if (tiles > cus && tiles % cus != 0) {
-      const int64_t k = (tiles + cus - 1) / cus;  // workgroups a CU
+  // Two row tiles a workgroup likewise at one MFMA row block (M <= 8 at
+  // group 64: several workgroups share a CU at once), down to 24 rows (M = 4
+  // up: 512 workgroups of 28 rows instead of 448 of 32, within noise).
+  if ((p->R == 1 || p->MB == 1) && batch == 1 && qmv_even_override() != 0) {
+    const int64_t full = 16 * p->R;
+    const int64_t wgs = (N + full - 1) / full;
+    if (wgs > cus && wgs % cus != 0) {
+      const int64_t k = (wgs + cus - 1) / cus;  // workgroups a CU
       const int64_t rw = (N + k * cus - 1) / (k * cus);
-      if (rw >= 12 && rw < 16) p->RW = (int)rw;
+      if (4 * rw >= 3 * full && rw < full) p->RW = (int)rw;
     }
   }
   p->NW = (int)((kt + p->TPW - 1) / p->TPW);

@@ -93,13 +93,14 @@ def test_qmv_one_row_shapes(O, mlxq_dev, dtype, M, N, K):
     (F16, 64, 2, 12345, 4096),    # odd N
     (BF16, 64, 1, 7001, 2048),    # 14 rows a workgroup (2 a CU on 256 CUs), a 1-row last one
     (F16, 64, 1, 13000, 1024),    # 13 rows a workgroup (4 a CU)
+    (BF16, 64, 3, 15000, 1024),   # two row tiles, 30 rows a workgroup (2 a CU)
 ])
 def test_qmm_small_m_shapes(O, mlxq_dev, dtype, gs, M, N, K):
     """Small-M shapes against float64, among them 9-16 activation rows at
     group 128 (one MFMA row block with 16-chunk x staging): the qmv plan for
     them has no compiled instance, and the call must go on to the tiled GEMM
-    rather than fail; and one-row plans whose 16-row tiles do not come out
-    a whole number a CU, which take 12-15 rows a workgroup."""
+    rather than fail; and plans whose workgroups do not come out a whole
+    number a CU, which take 12-15 (one row tile) or 24-31 rows (two)."""
     w = rng_t(O, (N, K), 15, dtype, 0.05)
     wq = O.quantize(w, gs, 4, dtype)
     x = rng_t(O, (M, K), 16, dtype)
