@@ -2053,7 +2053,11 @@ int launch_decode(const void* q, int B, int Hq, int Hkv, const uint32_t* kp, con
   if (ov >= 32 && ov <= MAXC && (ov & (ov - 1)) == 0) {
     chunk = ov;
   } else {
-    while (chunk > 128 && ((span + chunk - 1) / chunk) * B * Hkv < cus) chunk /= 2;
+    // halve the chunk while the launch leaves CUs without a workgroup, down
+    // to 128 keys, 64 at 8 bits and D <= 128 (the 1k fp16 8-bit decode: 8.47
+    // -> 8.22 us on MI355X; 4-bit and D 256 small grids measured slower at 64)
+    const int cmin = (BITS == 8 && D <= 128) ? 64 : 128;
+    while (chunk > cmin && ((span + chunk - 1) / chunk) * B * Hkv < cus) chunk /= 2;
   }
   // a ring row's window may start mid-chunk at the wrap point: one extra chunk
   MLXQ_CHECK((chunk & (chunk - 1)) == 0, "decode chunk must be a power of two");
