@@ -470,7 +470,7 @@ def main():
                                                          for m in (1, 4, 16, 64)]
         for M, N, K in shapes:
             ql, qb, qk = qmv_workload(M=M, N=N, K=K)
-            q_ms = timer.graph_step_ms(ql, 100, 10)
+            q_ms = timer.graph_step_ms(ql, 200, 20)
             qmm.append({"M": M, "N": N, "K": K, "us_per_call": round(q_ms * 1e3, 3),
                         "GB/s": round(qb / (q_ms * 1e-3) / 1e9, 1),
                         "pct_hbm_peak": round(100 * qb / (q_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 1),
@@ -488,7 +488,7 @@ def main():
     if run("ring"):
         log("bench: batched ring decode")
         l3, b3, k3 = batched_ring_workload()
-        ms3 = timer.graph_step_ms(l3, 50, 5)
+        ms3 = timer.graph_step_ms(l3, 200, 20)
         extra["decode_batched_ring"] = {"us_per_call": round(ms3 * 1e3, 3), "algorithmic_bytes": b3,
                                         "GB/s": round(b3 / (ms3 * 1e-3) / 1e9, 1),
                                         "pct_hbm_peak": round(100 * b3 / (ms3 * 1e-3) / 1e9 / HBM_PEAK_GBS, 1)}
@@ -498,7 +498,7 @@ def main():
         moe = {}
         for name, (n, k) in (("gate_up", (1408, 2816)), ("down", (2816, 704))):
             lm, bm, km = moe_gather_workload(n, k)
-            msm = timer.graph_step_ms(lm, 100, 10)
+            msm = timer.graph_step_ms(lm, 200, 20)
             moe[name] = {"N": n, "K": k, "us_per_call": round(msm * 1e3, 3), "algorithmic_bytes": bm,
                          "GB/s": round(bm / (msm * 1e-3) / 1e9, 1),
                          "pct_hbm_peak": round(100 * bm / (msm * 1e-3) / 1e9 / HBM_PEAK_GBS, 1)}
@@ -507,7 +507,7 @@ def main():
     if run("moe_sorted"):
         log("bench: MoE gather_qmm, sorted prefill rows")
         ls_, lr_, bs_, fs_, ks_ = moe_sorted_workload(1408, 2816)
-        mss = timer.graph_step_ms(ls_, 20, 3)
+        mss = timer.graph_step_ms(ls_, 50, 5)
         msr = timer.graph_step_ms(lr_, 5, 1)
         extra["moe_gather_prefill_sorted"] = {
             "workload": "gate_up [1408, 2816] 4-bit, 512 tokens x top-8 of 128 experts = 4096 rows in expert order",
@@ -518,7 +518,7 @@ def main():
     if run("tied_head"):
         log("bench: tied head")
         lh, bh, kh = tied_head_workload()
-        msh = timer.graph_step_ms(lh, 50, 5)
+        msh = timer.graph_step_ms(lh, 200, 10)
         extra["tied_head_qmv"] = {"workload": "x [1, 2816] @ W[262144, 2816]^T, 4-bit group 64",
                                   "us_per_call": round(msh * 1e3, 2), "algorithmic_bytes": bh,
                                   "GB/s": round(bh / (msh * 1e-3) / 1e9, 1),
@@ -536,7 +536,7 @@ def main():
         log("bench: gemma4 full attention (D 512)")
         g4 = {}
         lg, bg, kg = decode_workload(B=1, Hq=16, Hkv=2, D=512, N=32768, gs=64, bits=4)
-        msg = timer.graph_step_ms(lg, 100, 10)
+        msg = timer.graph_step_ms(lg, 200, 20)
         g4["decode_32k"] = {"us_per_call": round(msg * 1e3, 2), "algorithmic_bytes": bg,
                             "GB/s": round(bg / (msg * 1e-3) / 1e9, 1),
                             "pct_hbm_peak": round(100 * bg / (msg * 1e-3) / 1e9 / HBM_PEAK_GBS, 1)}
